@@ -1,0 +1,353 @@
+"""Benchmark of the quantized linear hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+
+Headline workload (one JSON line on stdout): the W8A8 QuantLinear forward with ConvRot at the
+Wan-14B FFN up-projection shape -- x [32760, 5120] bf16 (N(0,1), 1% of channels x20) ->
+fused rotate + per-token int8 quantize -> int8 MFMA GEMM with the dequant + bias epilogue ->
+y [32760, 13824] bf16.  A step is one forward of the module (both kernels); `value` is
+2*M*N*K / step time in TOPS with all inputs resident in HBM.
+
+`roofline` is the int8 GEMM kernel (the dominant one): algorithmic ops per launch divided by
+its average launch time, timed with HIP events around each launch on its stream during the
+timed steps.  `cpu_baseline` is the CPU oracle (the quantized-reference restatement in C with
+OpenMP) on a bounded sample of rows of the same workload, on this host's cores.
+
+`extra` carries the other shapes: the int4 (W4A16) text-encoder MLP at M=512 with an M sweep,
+the fp8 QKV projection, the 40-block Wan-14B linear stack, and the int8 weight-only layer.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "comfyui-powershard_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "W8A8 GEMM TOPS (% int8 MFMA peak) + int4 GEMM HBM GB/s; Wan-14B block ms"
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOPS
+PEAK_FP8_TFLOPS = 5000.0     # dense fp8
+PEAK_BF16_TFLOPS = 2500.0    # dense bf16
+PEAK_HBM_GBS = 8000.0        # HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample time")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------- inputs
+def gen(seed):
+    import torch
+    return torch.Generator(device="cuda").manual_seed(seed)
+
+
+def activations(M, K, cfg, outlier_scale=20.0, student_t=False, dev="cuda"):
+    """bf16 [M, K]: N(0,1) (or Student-t, df=3) with 1% of channels (seeded pick) scaled."""
+    import torch
+    g = gen(2000 + cfg)
+    x = torch.randn(M, K, generator=g, device=dev)
+    if student_t:
+        chi = torch.zeros_like(x)
+        for _ in range(3):
+            chi += torch.randn(M, K, generator=g, device=dev) ** 2
+        x /= (chi / 3).sqrt()
+    gp = torch.Generator().manual_seed(4000 + cfg)
+    idx = torch.randperm(K, generator=gp)[: int(0.01 * K)].to(dev)
+    x[:, idx] *= outlier_scale
+    return x.to(torch.bfloat16)
+
+
+def quant_layer(K, N, weight_format, cfg, seed=None, opts=None, dev="cuda"):
+    """A QuantLinear installed and filled through the package's own install/pack path."""
+    import torch
+    from torch import nn
+    from powershard_amd.quant_linear import install_quant_linears, quantized_from_float, pack
+    g = gen(1000 + cfg if seed is None else seed)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(N, generator=gen(3000 + cfg), device=dev) * 0.01).to(torch.bfloat16)
+    with torch.device("meta"):
+        net = nn.Sequential(nn.Linear(K, N, dtype=torch.bfloat16))
+    tensors = {"0.weight": {"key": "0.weight", "dtype": "BF16", "shape": [N, K]}}
+    install_quant_linears(net, tensors, weight_format, "native", None, torch.bfloat16, torch.device(dev),
+                          quant_options=opts)
+    layer = net[0]
+    qt = quantized_from_float(w, layer._ps_qplan.fmt, **(opts or {}))
+    layer.qbytes = nn.Parameter(pack(qt, layer._ps_qplan, dev), requires_grad=False)
+    layer.bias = nn.Parameter(b, requires_grad=False)
+    del w
+    return layer, qt, b
+
+
+# ---------------------------------------------------------------------- timing
+def timed_steps(step, steps, warmup):
+    """(ms per step from events around the whole loop, {kernel: mean ms per launch})."""
+    import torch
+    from powershard_amd import ops
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with ops.kernel_timer() as ev:
+        start.record()
+        for _ in range(steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+    total = start.elapsed_time(end)
+    per = {k: sum(v) / len(v) for k, v in ops.kernel_times_ms(ev).items()}
+    return total / steps, per
+
+
+def untimed_kernel_ms(step, steps, warmup):
+    """Same as timed_steps without per-launch events (pure step time)."""
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+# -------------------------------------------------------------------- workloads
+def headline(args):
+    import torch
+    M, K, N = 32760, 5120, 13824
+    cfg = 1
+    log(f"[bench] headline W8A8+ConvRot M={M} K={K} N={N}: building inputs")
+    x = activations(M, K, cfg)
+    layer, qt, b = quant_layer(K, N, "int8", cfg, opts={"convrot": True, "convrot_groupsize": 256})
+    with torch.no_grad():
+        y = layer(x)
+    if not layer._ps_native:
+        raise RuntimeError("native path fell back to dequantize")
+    log(f"[bench] headline: warmup {args.warmup}, timing {args.steps} steps")
+
+    def step():
+        with torch.no_grad():
+            layer(x)
+    ms, per = timed_steps(step, args.steps, args.warmup)
+    ms_clean = untimed_kernel_ms(step, args.steps, 2)
+    ops_per_step = 2.0 * M * N * K
+    gemm_ms = per["gemm_i8"]
+    quant_ms = per["quantize_rows_i8"]
+    tops = ops_per_step / (ms_clean * 1e-3) / 1e12
+    gemm_tops = ops_per_step / (gemm_ms * 1e-3) / 1e12
+    quant_bytes = M * K * 2 + M * K + M * 4
+    res = dict(M=M, N=N, K=K, ms_per_step=ms_clean, ms_per_step_with_events=ms, tops=tops, gemm_ms=gemm_ms,
+               gemm_tops=gemm_tops, quant_ms=quant_ms, quant_gbs=quant_bytes / (quant_ms * 1e-3) / 1e9,
+               quant_bytes=quant_bytes)
+    log(f"[bench] headline: {ms_clean:.3f} ms/step, {tops:.1f} TOPS; gemm {gemm_ms:.3f} ms = {gemm_tops:.1f} TOPS "
+        f"({100 * gemm_tops / PEAK_INT8_TOPS:.1f}% of int8 peak); quant {quant_ms * 1e3:.1f} us = "
+        f"{res['quant_gbs']:.0f} GB/s")
+    sample = dict(x=x[:512].cpu(), qdata=qt._qdata.cpu(), scale=qt._params.scale.cpu(), bias=b.cpu(), y=y[:512].cpu())
+    del layer, qt, x, y
+    torch.cuda.empty_cache()
+    return res, sample
+
+
+def check_headline_parity(sample):
+    """Bit-exact check of the headline's first rows against the oracle (quant + int32 + epilogue)."""
+    import torch
+    import oracle
+    rows = 64
+    qa, sa = oracle.quantize_rows_i8(sample["x"][:rows], 256)
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, sample["qdata"]), sa, sample["scale"], sample["bias"])
+    got = sample["y"][:rows]
+    same = bool(torch.equal(got.view(torch.int16), ref.view(torch.int16)))
+    err = (got.float() - ref.float()).abs().max().item()
+    rms = ref.float().pow(2).mean().sqrt().item()
+    return dict(rows_checked=rows, bitexact=same, max_abs_err_over_rms=err / rms)
+
+
+def cpu_baseline(sample, target_s):
+    """Oracle (C, OpenMP, all affinity cores) W8A8 forward on a bounded row sample."""
+    import torch
+    import oracle
+    N, K = sample["qdata"].shape
+    threads = oracle.num_threads()
+    x = sample["x"]
+    rows = 8
+    while True:
+        t0 = time.perf_counter()
+        qa, sa = oracle.quantize_rows_i8(x[:rows], 256)
+        y = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, sample["qdata"]), sa, sample["scale"], sample["bias"])
+        dt = time.perf_counter() - t0
+        if dt * 4 > target_s or rows >= x.shape[0]:
+            break
+        rows = min(x.shape[0], rows * 4)
+    del y
+    tops = 2.0 * rows * N * K / dt / 1e12
+    return dict(value=tops, unit="TOPS", cores=threads, kind="port",
+                sample=f"W8A8+ConvRot forward (rotate+quantize, int32 GEMM, epilogue) of {rows} token rows x "
+                       f"{N}x{K} weights, {dt:.2f} s on {threads} threads; same synthetic inputs as the GPU run")
+
+
+def extra_int4(args):
+    """W4A16 uint4 g128 Qwen3-VL-32B text-encoder MLP, K=5120 -> N=25600; M sweep; MALL-defeating
+    rotation over 4 distinct weight copies (4 x 69.6 MB > 256 MB Infinity Cache)."""
+    import torch
+    K, N, cfg = 5120, 25600, 2
+    layers = [quant_layer(K, N, "int4", cfg, seed=1000 + cfg + 17 * i, opts={"group_size": 128})[0] for i in range(4)]
+    out = {}
+    for M in (1, 16, 64, 128, 256, 512):
+        x = activations(M, K, cfg, outlier_scale=1.0)
+        it = [0]
+
+        def step():
+            with torch.no_grad():
+                layers[it[0] % 4](x)
+            it[0] += 1
+        ms, per = timed_steps(step, max(args.steps, 20), args.warmup)
+        kms = per["gemm_w4a16"]
+        wbytes = N * K // 2 + 2 * 2 * N * (K // 128)
+        algo_bytes = wbytes + M * K * 2 + M * N * 2
+        flops = 2.0 * M * N * K
+        out[M] = dict(kernel_ms=kms, hbm_gbs=algo_bytes / (kms * 1e-3) / 1e9,
+                      hbm_frac=algo_bytes / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                      tflops=flops / (kms * 1e-3) / 1e12, bf16_mfma_frac=flops / (kms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS)
+        log(f"[bench] int4 M={M}: {kms * 1e3:.1f} us, {out[M]['hbm_gbs']:.0f} GB/s, {out[M]['tflops']:.1f} TFLOP/s")
+    del layers
+    torch.cuda.empty_cache()
+    return dict(workload="W4A16 uint4 asym g128, K=5120->N=25600", sweep=out)
+
+
+def extra_fp8(args):
+    import torch
+    M, K, N, cfg = 32760, 5120, 15360, 3
+    x = activations(M, K, cfg, outlier_scale=1.0)
+    layer = quant_layer(K, N, "fp8", cfg)[0]
+
+    def step():
+        with torch.no_grad():
+            layer(x)
+    ms, per = timed_steps(step, args.steps, args.warmup)
+    flops = 2.0 * M * N * K
+    res = dict(workload="fp8 e4m3 per-token x per-tensor, Wan-14B QKV 5120->15360, M=32760", ms_per_step=ms,
+               tflops=flops / (ms * 1e-3) / 1e12, gemm_ms=per["gemm_fp8"],
+               gemm_tflops=flops / (per["gemm_fp8"] * 1e-3) / 1e12,
+               gemm_frac=flops / (per["gemm_fp8"] * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
+               quant_ms=per["quantize_rows_fp8"])
+    log(f"[bench] fp8: {ms:.3f} ms/step, gemm {res['gemm_tflops']:.0f} TFLOP/s ({100 * res['gemm_frac']:.1f}%)")
+    del layer, x
+    torch.cuda.empty_cache()
+    return res
+
+
+def extra_wan_stack(args):
+    """40 Wan-14B blocks of W8A8+ConvRot linears at M=32760 (q, k, v, o, ffn up, ffn down);
+    heavy-tailed inputs (Student-t df=3, 1% channels x50); random-init int8 weights per block."""
+    import torch
+    M, D, F, cfg = 32760, 5120, 13824, 4
+    opts = {"convrot": True, "convrot_groupsize": 256}
+    blocks = []
+    for blk in range(40):
+        seed = 1000 + cfg + 1000 * blk
+        q = quant_layer(D, D, "int8", cfg, seed=seed + 1, opts=opts)[0]
+        k = quant_layer(D, D, "int8", cfg, seed=seed + 2, opts=opts)[0]
+        v = quant_layer(D, D, "int8", cfg, seed=seed + 3, opts=opts)[0]
+        o = quant_layer(D, D, "int8", cfg, seed=seed + 4, opts=opts)[0]
+        up = quant_layer(D, F, "int8", cfg, seed=seed + 5, opts=opts)[0]
+        down = quant_layer(F, D, "int8", cfg, seed=seed + 6, opts=opts)[0]
+        blocks.append((q, k, v, o, up, down))
+    x = activations(M, D, cfg, outlier_scale=50.0, student_t=True)
+    h = activations(M, F, cfg + 100, outlier_scale=50.0, student_t=True)
+
+    def step():
+        with torch.no_grad():
+            for q, k, v, o, up, down in blocks:
+                q(x); k(x); v(x); o(x); up(x); down(h)
+    steps = max(2, min(args.steps, 3))
+    ms, per = timed_steps(step, steps, 1)
+    ops_per_block = 2.0 * M * (4 * D * D + 2 * D * F)
+    res = dict(workload="40 Wan-14B blocks (q,k,v,o 5120^2; ffn 5120<->13824) W8A8+ConvRot, M=32760",
+               ms_total=ms, ms_per_block=ms / 40, tops=40 * ops_per_block / (ms * 1e-3) / 1e12,
+               frac_int8_peak=40 * ops_per_block / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+               quant_ms_mean=per["quantize_rows_i8"], gemm_ms_mean=per["gemm_i8"])
+    log(f"[bench] wan stack: {ms:.1f} ms total, {ms / 40:.2f} ms/block, {res['tops']:.0f} TOPS")
+    del blocks, x, h
+    torch.cuda.empty_cache()
+    return res
+
+
+def extra_w8a16(args):
+    import torch
+    M, K, N, cfg = 1024, 5120, 5120, 0
+    from powershard_amd import ops
+    x = activations(M, K, cfg, outlier_scale=1.0)
+    layer, qt, b = quant_layer(K, N, "int8", cfg)
+    q, s = qt._qdata, qt._params.scale
+
+    def step():
+        ops.gemm_w8a16(x, q, s, b)
+    ms, per = timed_steps(step, max(args.steps, 20), args.warmup)
+    flops = 2.0 * M * N * K
+    res = dict(workload="int8 weight-only (W8A16) 1024x5120x5120", kernel_ms=per["gemm_w8a16"],
+               tflops=flops / (per["gemm_w8a16"] * 1e-3) / 1e12)
+    log(f"[bench] w8a16: {per['gemm_w8a16'] * 1e3:.1f} us, {res['tflops']:.0f} TFLOP/s")
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU: the quantized linear path has no multi-GPU "
+                                   "code (see DESIGN.md for how it would shard); run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    from powershard_amd import _native
+    _native.lib()
+    h, sample = headline(args)
+    parity = check_headline_parity(sample)
+    log(f"[bench] headline parity (64 rows vs oracle): {parity}")
+    cpu = None if args.no_cpu else cpu_baseline(sample, args.cpu_seconds)
+    if cpu:
+        log(f"[bench] cpu baseline: {cpu['value'] * 1e3:.1f} GOPS on {cpu['cores']} threads")
+    extra = {}
+    if not args.no_extra:
+        for name, fn in (("int4_w4a16", extra_int4), ("fp8", extra_fp8), ("w8a16", extra_w8a16),
+                         ("wan14b_stack", extra_wan_stack)):
+            try:
+                extra[name] = fn(args)
+            except torch.cuda.OutOfMemoryError as e:
+                extra[name] = {"error": f"OOM: {e}"}
+    roof = dict(bound="mfma", achieved=h["gemm_tops"], peak=PEAK_INT8_TOPS, unit="TOPS",
+                frac=h["gemm_tops"] / PEAK_INT8_TOPS, traffic=None, kernel="gemm_i8",
+                kernel_ms=h["gemm_ms"], algorithmic_ops_per_launch=2.0 * h["M"] * h["N"] * h["K"])
+    line = {
+        "metric": METRIC, "value": round(h["tops"], 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(h["ms_per_step"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "W8A8 QuantLinear forward with ConvRot (rotate+quantize, int8 MFMA GEMM, "
+                               "dequant+bias epilogue), Wan-14B FFN up 5120->13824, M=32760 tokens",
+                   "M": h["M"], "K": h["K"], "N": h["N"], "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": {"gemm_i8_ms": h["gemm_ms"], "quantize_rows_i8_ms": h["quant_ms"],
+                    "quantize_rows_i8_gbs": h["quant_gbs"]},
+        "parity": parity,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

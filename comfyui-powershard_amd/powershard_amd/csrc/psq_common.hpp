@@ -1,0 +1,210 @@
+// psq_common.hpp -- shared device helpers of libpsquant (gfx950 only).
+//
+// Scalar formats follow the conventions of the library's C ABI (include/psquant.h):
+// bf16 / fp16 round-to-nearest-even, OCP fp8 e4m3fn with saturation to +-448.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+
+#include "../../../include/psquant.h"
+
+namespace psq {
+
+// ------------------------------------------------------------------ host-side errors
+// Records the message of the last failure on this thread and returns `code`.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Checks the launch of the kernel just issued.
+int check_launch(const char *what);
+
+// Validates the current device (gfx950) once per device; 0 or PSQ_E_DEVICE.
+int require_device();
+
+inline bool valid_dtype(int dt) { return dt == PSQ_BF16 || dt == PSQ_F16 || dt == PSQ_F32; }
+
+// ------------------------------------------------------------------ vector types
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+// ------------------------------------------------------------------ scalar formats
+__device__ __forceinline__ float bf16_to_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x0040u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h16)
+{
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)h16);
+    return (float)h;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16(float f)
+{
+    _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// Convert one 16-bit element of dtype DT (bf16 or f16) held in the low half of `h`.
+template <int DT>
+__device__ __forceinline__ float half_to_f32(uint32_t h)
+{
+    if constexpr (DT == PSQ_BF16) return bf16_to_f32(h & 0xffffu);
+    else return f16_to_f32(h & 0xffffu);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t f32_to_half(float f)
+{
+    if constexpr (DT == PSQ_BF16) return f32_to_bf16(f);
+    else return f32_to_f16(f);
+}
+
+// OCP e4m3fn decode.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c)
+{
+    uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+    float v;
+    if (e == 0) v = (float)m * 0x1p-9f;
+    else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    if (e == 0xf && m == 7) v = __builtin_nanf("");
+    return (c & 0x80u) ? -v : v;
+}
+
+// OCP e4m3fn encode, round to nearest even, saturating to +-448 (callers clamp first).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x)
+{
+    uint32_t u = __float_as_uint(x);
+    uint32_t sign = (u >> 24) & 0x80u;
+    uint32_t au = u & 0x7fffffffu;
+    float a = __uint_as_float(au);
+    uint32_t code;
+    if (au > 0x7f800000u) return 0x7fu;
+    if (a >= 448.0f) {
+        code = 0x7eu;
+    } else if (a < 0x1p-6f) {
+        code = (uint32_t)__builtin_rintf(a * 512.0f);          // subnormal steps of 2^-9
+    } else {
+        uint32_t r = au + 0x7ffffu + ((au >> 20) & 1u);          // RNE at mantissa bit 20
+        code = (r >> 20) - (120u << 3);                          // rebias 127 -> 7
+    }
+    return sign | code;
+}
+
+// ------------------------------------------------------------------ stores
+// Store one fp32 value as element i of an output of dtype dt.
+__device__ __forceinline__ void store_elem(void *p, int64_t i, int dt, float v)
+{
+    if (dt == PSQ_BF16) ((uint16_t *)p)[i] = (uint16_t)f32_to_bf16(v);
+    else if (dt == PSQ_F16) ((uint16_t *)p)[i] = (uint16_t)f32_to_f16(v);
+    else ((float *)p)[i] = v;
+}
+
+__device__ __forceinline__ float load_elem(const void *p, int64_t i, int dt)
+{
+    if (dt == PSQ_BF16) return bf16_to_f32(((const uint16_t *)p)[i]);
+    if (dt == PSQ_F16) return f16_to_f32(((const uint16_t *)p)[i]);
+    return ((const float *)p)[i];
+}
+
+// ------------------------------------------------------------------ cross-lane moves
+// DPP permutations inside a row of 16 lanes (no LDS traffic).
+enum : int {
+    DPP_QUAD_XOR1 = 0xB1,        // quad_perm [1,0,3,2]
+    DPP_QUAD_XOR2 = 0x4E,        // quad_perm [2,3,0,1]
+    DPP_QUAD_XOR3 = 0x1B,        // quad_perm [3,2,1,0]
+    DPP_ROW_MIRROR = 0x140,      // lane ^ 15 within a row of 16
+    DPP_ROW_HALF_MIRROR = 0x141, // lane ^ 7 within a half row of 8
+    DPP_ROW_ROR8 = 0x128         // lane ^ 8 within a row of 16
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// value of lane ^ (m * L) for the three radix-4 partners at lane stride L in {1, 4}
+template <int L, int M_>
+__device__ __forceinline__ float lane_xor(float v)
+{
+    if constexpr (L == 1) {
+        if constexpr (M_ == 1) return dpp<DPP_QUAD_XOR1>(v);
+        else if constexpr (M_ == 2) return dpp<DPP_QUAD_XOR2>(v);
+        else return dpp<DPP_QUAD_XOR3>(v);
+    } else if constexpr (L == 4) {
+        if constexpr (M_ == 1) return dpp<DPP_QUAD_XOR3>(dpp<DPP_ROW_HALF_MIRROR>(v));  // ^7 ^3 = ^4
+        else if constexpr (M_ == 2) return dpp<DPP_ROW_ROR8>(v);                          // ^8
+        else return dpp<DPP_QUAD_XOR3>(dpp<DPP_ROW_MIRROR>(v));                           // ^15 ^3 = ^12
+    } else {
+        return __shfl_xor(v, L * M_, 64);
+    }
+}
+
+// wave-wide max of non-negative values
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        float w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// ------------------------------------------------------------------ radix-4 ConvRot stage
+// y_j = S - 2 x_{3-j} with S = (x0 + x1) + (x2 + x3): one stage of the unnormalized regular
+// Hadamard transform (H4[a][b] = -1 iff a + b == 3).
+__device__ __forceinline__ void radix4(float &x0, float &x1, float &x2, float &x3)
+{
+    float s01 = x0 + x1;
+    float s23 = x2 + x3;
+    float s = s01 + s23;
+    float y0 = s - 2.0f * x3;
+    float y1 = s - 2.0f * x2;
+    float y2 = s - 2.0f * x1;
+    float y3 = s - 2.0f * x0;
+    x0 = y0; x1 = y1; x2 = y2; x3 = y3;
+}
+
+// Same stage across the four lanes whose lane index differs in the base-4 digit of weight L.
+template <int L>
+__device__ __forceinline__ float radix4_lanes(float x)
+{
+    float t = x + lane_xor<L, 1>(x);   // x_{d} + x_{d^1}: (x0+x1) or (x2+x3), commutative
+    float s = t + lane_xor<L, 2>(t);   // (x0+x1) + (x2+x3)
+    float r = lane_xor<L, 3>(x);       // x_{3-d}
+    return s - 2.0f * r;
+}
+
+// ------------------------------------------------------------------ XCD-aware tile order
+// gfx950 dispatches workgroup i to XCD (i % 8).  Re-number so that each XCD receives a
+// contiguous range of logical tiles, then walk tiles in groups of `group_m` tile rows so
+// that concurrently resident tiles of one XCD share A rows and W rows in its L2.
+__device__ __forceinline__ void tile_order(int pid, int nbm, int nbn, int group_m, int &pm, int &pn)
+{
+    const int nblk = nbm * nbn;
+    const int xcd = pid & 7, per = nblk >> 3, rem = nblk & 7;
+    int lid = xcd * per + (xcd < rem ? xcd : rem) + (pid >> 3);
+    const int in_group = group_m * nbn;
+    const int gid = lid / in_group;
+    const int first_m = gid * group_m;
+    const int gsz = (nbm - first_m) < group_m ? (nbm - first_m) : group_m;
+    const int r = lid - gid * in_group;
+    pm = first_m + r % gsz;
+    pn = r / gsz;
+}
+
+}  // namespace psq

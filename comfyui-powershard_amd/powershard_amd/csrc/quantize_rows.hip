@@ -1,0 +1,218 @@
+// quantize_rows.hip -- fused ConvRot rotation + per-token absmax + int8 / fp8 quantization.
+//
+// The activation side of W8A8 (comfy-kitchen int8_linear / QuantizedTensor.from_float,
+// reached from powershard/quant_linear.py:233-236) and of the fp8 scaled-mm path.
+// Conventions (bit-exact with the CPU oracle):
+//   u = T(x): unnormalized regular-Hadamard transform per group of g = 4^k elements
+//     (x H = 2^-k T(x), H from powershard/operations.py:72-81), radix-4 stages over base-4
+//     digits, least significant digit first, S = (x0 + x1) + (x2 + x3), y_j = S - 2 x_{3-j};
+//   a = max |u| over the row; a == 0 -> s = 1, q = 0; else r = LIM / a, s = (a / LIM) 2^-k;
+//   static input scale: s = s_in, r = (1 / s_in) 2^-k;
+//   int8: q = clamp(rint(u r), -127, 127);  fp8: q = e4m3_rne(clamp(u r, -448, 448)).
+//
+// Layout: one workgroup per row (token), one thread per 16 consecutive elements (32 bytes of
+// bf16 in, 16 bytes of codes out; both fully coalesced).  Base-4 digits 0 and 1 of the element
+// index live inside a thread, digit 2 on lane bits 0-1 (DPP quad permutes), digit 3 on lane bits
+// 2-3 (DPP row mirrors/rotates), digit 4 on lane bits 4-5 (cross-lane shuffle; g = 1024 only).
+// The row's absmax is reduced across the wave with shuffles and across waves through LDS.
+// HBM-bound: 2 bytes read + 1 byte written per element (+4 bytes per row).
+#include "psq_common.hpp"
+
+namespace psq {
+namespace {
+
+constexpr int kElemsPerThread = 16;
+constexpr int kMaxThreads = 1024;
+constexpr int kMaxK = kElemsPerThread * kMaxThreads;
+
+template <int DT>
+__device__ __forceinline__ void load16(const uint16_t *__restrict__ src, bool active, float (&v)[16])
+{
+    v4i lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+    if (active) {
+        lo = *(const v4i *)(src);
+        hi = *(const v4i *)(src + 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t a = (uint32_t)lo[i], b = (uint32_t)hi[i];
+        v[2 * i] = half_to_f32<DT>(a);
+        v[2 * i + 1] = half_to_f32<DT>(a >> 16);
+        v[8 + 2 * i] = half_to_f32<DT>(b);
+        v[8 + 2 * i + 1] = half_to_f32<DT>(b >> 16);
+    }
+}
+
+// Unnormalized transform of the 16 values of this thread (in-thread digits) and of the
+// cross-lane digits, for a group size of 4^ROTK.
+template <int ROTK>
+__device__ __forceinline__ void rotate16(float (&v)[16])
+{
+    if constexpr (ROTK >= 1) {
+#pragma unroll
+        for (int b = 0; b < 16; b += 4) radix4(v[b], v[b + 1], v[b + 2], v[b + 3]);
+    }
+    if constexpr (ROTK >= 2) {
+#pragma unroll
+        for (int a = 0; a < 4; a++) radix4(v[a], v[a + 4], v[a + 8], v[a + 12]);
+    }
+    if constexpr (ROTK >= 3) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<1>(v[j]);
+    }
+    if constexpr (ROTK >= 4) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<4>(v[j]);
+    }
+    if constexpr (ROTK >= 5) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<16>(v[j]);
+    }
+}
+
+template <int DT, int ROTK, bool FP8>
+__global__ void __launch_bounds__(kMaxThreads)
+quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int K,
+                     const float *__restrict__ static_scale, uint8_t *__restrict__ q, int64_t ldq,
+                     float *__restrict__ scale)
+{
+    __shared__ float wave_amax[kMaxThreads / 64];
+    const int64_t row = blockIdx.x;
+    const int t = threadIdx.x;
+    const bool active = t * kElemsPerThread < K;
+    constexpr float LIM = FP8 ? 448.0f : 127.0f;
+    const float post = ROTK ? __builtin_ldexpf(1.0f, -ROTK) : 1.0f;
+
+    float v[16];
+    load16<DT>(x + row * ldx + (int64_t)t * kElemsPerThread, active, v);
+    rotate16<ROTK>(v);
+
+    float r, s;
+    if (static_scale) {
+        s = *static_scale;
+        r = (1.0f / s) * post;
+    } else {
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            float a = __builtin_fabsf(v[j]);
+            amax = a > amax ? a : amax;
+        }
+        amax = wave_max(amax);
+        const int nw = (blockDim.x + 63) >> 6;
+        if ((t & 63) == 0) wave_amax[t >> 6] = amax;
+        __syncthreads();
+        amax = wave_amax[0];
+        for (int w = 1; w < nw; w++) {
+            float b = wave_amax[w];
+            amax = b > amax ? b : amax;
+        }
+        if (amax == 0.0f) {
+            s = 1.0f;
+            r = 1.0f;
+        } else {
+            r = LIM / amax;
+            s = (amax / LIM) * post;
+        }
+    }
+    if (t == 0) scale[row] = s;
+    if (!active) return;
+
+    uint32_t packed[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            float u = v[4 * i + b] * r;
+            uint32_t code;
+            if constexpr (FP8) {
+                u = __builtin_fminf(__builtin_fmaxf(u, -448.0f), 448.0f);
+                code = f32_to_e4m3(u);
+            } else {
+                u = __builtin_rintf(u);
+                u = __builtin_fminf(__builtin_fmaxf(u, -127.0f), 127.0f);
+                code = (uint32_t)(int32_t)u & 0xffu;
+            }
+            word |= code << (8 * b);
+        }
+        packed[i] = word;
+    }
+    v4i out = {(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
+    *(v4i *)(q + row * ldq + (int64_t)t * kElemsPerThread) = out;
+}
+
+template <int DT, bool FP8>
+int launch_quant(const void *x, int64_t M, int64_t K, int64_t ldx, int rotk,
+                 const float *static_scale, uint8_t *q, int64_t ldq, float *scale, hipStream_t st)
+{
+    const int threads = (int)(((K / kElemsPerThread) + 63) / 64 * 64);
+    const dim3 grid((unsigned)M), block(threads);
+    const uint16_t *xp = (const uint16_t *)x;
+    switch (rotk) {
+#define PSQ_CASE(RK)                                                                        \
+    case RK:                                                                                \
+        quantize_rows_kernel<DT, RK, FP8><<<grid, block, 0, st>>>(xp, ldx, (int)K,          \
+                                                                  static_scale, q, ldq, scale); \
+        break;
+        PSQ_CASE(0) PSQ_CASE(1) PSQ_CASE(2) PSQ_CASE(3) PSQ_CASE(4) PSQ_CASE(5)
+#undef PSQ_CASE
+    default:
+        return set_error(PSQ_E_SHAPE, "rotation group 4^%d unsupported", rotk);
+    }
+    return check_launch(FP8 ? "quantize_rows_fp8" : "quantize_rows_i8");
+}
+
+int quantize_rows(bool fp8, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  int rot_group, const float *static_scale, uint8_t *q, int64_t ldq, float *scale,
+                  void *stream)
+{
+    if (M < 0 || K < 0) return set_error(PSQ_E_ARG, "negative size M=%lld K=%lld", (long long)M, (long long)K);
+    if (M == 0) return PSQ_OK;
+    if (!x || !q || !scale) return set_error(PSQ_E_ARG, "null pointer");
+    if (x_dtype != PSQ_BF16 && x_dtype != PSQ_F16)
+        return set_error(PSQ_E_ARG, "activations must be bf16 or f16 (dtype %d)", x_dtype);
+    if (K == 0 || K % kElemsPerThread || K > kMaxK)
+        return set_error(PSQ_E_SHAPE, "K=%lld must be a positive multiple of 16 and <= %d", (long long)K, kMaxK);
+    if (ldx < K || ldq < K || ldx % 8 || ldq % 16)
+        return set_error(PSQ_E_SHAPE, "strides ldx=%lld (mult. of 8) ldq=%lld (mult. of 16) must cover K=%lld",
+                         (long long)ldx, (long long)ldq, (long long)K);
+    if (((uintptr_t)x & 15) || ((uintptr_t)q & 15))
+        return set_error(PSQ_E_SHAPE, "x and q must be 16-byte aligned");
+    if (M > 0x7fffffffLL) return set_error(PSQ_E_SHAPE, "M=%lld too large", (long long)M);
+    int rotk = 0;
+    if (rot_group) {
+        int g = rot_group;
+        while (g > 1 && (g & 3) == 0) { g >>= 2; rotk++; }
+        if (g != 1 || rotk < 1 || rotk > 5 || K % rot_group)
+            return set_error(PSQ_E_SHAPE, "rotation group %d must be a power of 4 in [4,1024] dividing K=%lld",
+                             rot_group, (long long)K);
+    }
+    if (int e = require_device()) return e;
+    hipStream_t st = (hipStream_t)stream;
+    if (fp8)
+        return x_dtype == PSQ_BF16 ? launch_quant<PSQ_BF16, true>(x, M, K, ldx, rotk, static_scale, q, ldq, scale, st)
+                                   : launch_quant<PSQ_F16, true>(x, M, K, ldx, rotk, static_scale, q, ldq, scale, st);
+    return x_dtype == PSQ_BF16 ? launch_quant<PSQ_BF16, false>(x, M, K, ldx, rotk, static_scale, q, ldq, scale, st)
+                               : launch_quant<PSQ_F16, false>(x, M, K, ldx, rotk, static_scale, q, ldq, scale, st);
+}
+
+}  // namespace
+}  // namespace psq
+
+extern "C" {
+
+int psq_quantize_rows_i8(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int rot_group,
+                         const float *static_scale, int8_t *q, int64_t ldq, float *scale, void *stream)
+{
+    return psq::quantize_rows(false, x, x_dtype, M, K, ldx, rot_group, static_scale, (uint8_t *)q, ldq,
+                              scale, stream);
+}
+
+int psq_quantize_rows_fp8(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int rot_group,
+                          const float *static_scale, uint8_t *q, int64_t ldq, float *scale, void *stream)
+{
+    return psq::quantize_rows(true, x, x_dtype, M, K, ldx, rot_group, static_scale, q, ldq, scale, stream);
+}
+
+}  // extern "C"

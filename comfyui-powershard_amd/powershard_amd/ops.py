@@ -1,0 +1,240 @@
+"""Torch-facing wrappers of the gfx950 kernels (device tensors in, device tensors out).
+
+Each op checks dtypes, devices and contiguity, allocates its outputs with PyTorch's caching
+allocator on the input's device, launches on that device's current stream and raises
+``RuntimeError`` (with the library's message) on any failure.  No op has a CPU implementation:
+on a tensor that is not on a GPU they raise ``RuntimeError``.
+"""
+import contextlib
+import ctypes
+
+import torch
+
+from . import _native
+
+# Opt-in launch timing: while kernel_timer() is active, every launch is bracketed by a pair of
+# HIP events recorded on the stream it runs on (the device's current stream).
+_timer = None
+
+
+@contextlib.contextmanager
+def kernel_timer():
+    """Collect {op name: [(start event, end event), ...]} for the launches inside the block."""
+    global _timer
+    prev, _timer = _timer, {}
+    try:
+        yield _timer
+    finally:
+        _timer = prev
+
+
+def kernel_times_ms(events):
+    """{op: [milliseconds per launch]} from kernel_timer()'s events (synchronizes)."""
+    torch.cuda.synchronize()
+    return {k: [a.elapsed_time(b) for a, b in v] for k, v in events.items()}
+
+
+def _launch(name, fn, *args):
+    if _timer is None:
+        return _native.check(fn(*args), name)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    status = fn(*args)
+    b.record()
+    _timer.setdefault(name, []).append((a, b))
+    return _native.check(status, name)
+
+_DT = {torch.bfloat16: _native.BF16, torch.float16: _native.F16, torch.float32: _native.F32}
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need_gpu(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(f"psquant kernels need GPU tensors (got {t.device})")
+
+
+def _dt(t, what):
+    if t.dtype not in _DT:
+        raise TypeError(f"{what}: unsupported dtype {t.dtype}")
+    return _DT[t.dtype]
+
+
+def _rows2d(x):
+    """[M, K] view with unit column stride and 16-byte aligned rows (copies if needed)."""
+    if x.dim() != 2:
+        raise ValueError("expected a 2-D tensor")
+    if x.stride(1) != 1 or (x.stride(0) * x.element_size()) % 16 or x.data_ptr() % 16:
+        x = x.contiguous()
+    return x
+
+
+def _bias(bias, n, device):
+    if bias is None:
+        return None, 0
+    if bias.numel() != n:
+        raise ValueError(f"bias has {bias.numel()} elements, expected {n}")
+    bias = bias.to(device).contiguous()
+    return bias, _dt(bias, "bias")
+
+
+# ------------------------------------------------------------------ activations
+def quantize_rows(x, fp8=False, rot_group=0, static_scale=None):
+    """Fused ConvRot rotation + per-row absmax + int8 (or fp8 e4m3fn) quantization.
+
+    x: [M, K] bf16/f16 on the GPU.  Returns (q [M, K] int8 or float8_e4m3fn, scale [M] fp32).
+    static_scale: optional fp32 tensor with one element (the module's input_scale).
+    """
+    _need_gpu(x, static_scale)
+    x = _rows2d(x)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"quantize_rows: activations must be bf16/f16, got {x.dtype}")
+    M, K = x.shape
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn if fp8 else torch.int8, device=x.device)
+    scale = torch.empty(M, dtype=torch.float32, device=x.device)
+    st = None
+    if static_scale is not None:
+        st = static_scale.to(device=x.device, dtype=torch.float32).reshape(-1)[:1].contiguous()
+    fn = _native.lib().psq_quantize_rows_fp8 if fp8 else _native.lib().psq_quantize_rows_i8
+    _launch("quantize_rows_fp8" if fp8 else "quantize_rows_i8", fn, _p(x), _DT[x.dtype], M, K, x.stride(0),
+            int(rot_group or 0), _p(st), _p(q), K, _p(scale), _stream(x))
+    return q, scale
+
+
+# ----------------------------------------------------------------------- GEMMs
+def gemm_i8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16):
+    """y = round(fmaf(a @ w.T (int32), a_scale[m] * w_scale[n], bias[n])): [M, N] out_dtype."""
+    _need_gpu(a, a_scale, w, w_scale)
+    a, w = _rows2d(a), _rows2d(w)
+    if a.dtype != torch.int8 or w.dtype != torch.int8:
+        raise TypeError("gemm_i8: operands must be int8")
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"gemm_i8: K mismatch {K} vs {w.shape[1]}")
+    a_scale = a_scale.to(torch.float32).reshape(-1).contiguous()
+    w_scale = w_scale.to(torch.float32).reshape(-1).contiguous()
+    if a_scale.numel() != M or w_scale.numel() != N:
+        raise ValueError("gemm_i8: scale sizes do not match M / N")
+    bias, bdt = _bias(bias, N, a.device)
+    y = torch.empty(M, N, dtype=out_dtype, device=a.device)
+    _launch("gemm_i8", _native.lib().psq_gemm_i8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale), _p(bias),
+                                            bdt, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
+    return y
+
+
+def gemm_i8_i32(a, w):
+    """Raw int32 accumulators a @ w.T ([M, N] int32)."""
+    _need_gpu(a, w)
+    a, w = _rows2d(a), _rows2d(w)
+    M, K = a.shape
+    N = w.shape[0]
+    c = torch.empty(M, N, dtype=torch.int32, device=a.device)
+    _launch("gemm_i8_i32", _native.lib().psq_gemm_i8_i32, _p(a), a.stride(0), _p(w), w.stride(0), _p(c), N, M, N, K, _stream(a))
+    return c
+
+
+def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16):
+    """fp8 e4m3fn GEMM: y = round(fmaf(a @ w.T (fp32), a_scale[m] * w_scale[n or 0], bias[n]))."""
+    _need_gpu(a, a_scale, w, w_scale)
+    a, w = _rows2d(a), _rows2d(w)
+    for t in (a, w):
+        if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
+            raise TypeError("gemm_fp8: operands must be float8_e4m3fn")
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"gemm_fp8: K mismatch {K} vs {w.shape[1]}")
+    a_scale = a_scale.to(torch.float32).reshape(-1).contiguous()
+    w_scale = w_scale.to(device=a.device, dtype=torch.float32).reshape(-1).contiguous()
+    if a_scale.numel() != M or w_scale.numel() not in (1, N):
+        raise ValueError("gemm_fp8: scale sizes do not match")
+    bias, bdt = _bias(bias, N, a.device)
+    y = torch.empty(M, N, dtype=out_dtype, device=a.device)
+    _launch("gemm_fp8", _native.lib().psq_gemm_fp8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale),
+                                             int(w_scale.numel() > 1), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K,
+                                             _stream(a))
+    return y
+
+
+def gemm_w4a16(x, wq, w_scale, w_zero, group_size, bias=None, out_dtype=None):
+    """uint4 asymmetric group weights, in-register dequantized onto bf16/f16 MFMA.
+
+    x [M, K] bf16/f16, wq [N, K/2] uint8 (low nibble = even k), w_scale/w_zero [N, K/group] fp16.
+    """
+    _need_gpu(x, wq, w_scale, w_zero)
+    x, wq = _rows2d(x), wq.contiguous()
+    M, K = x.shape
+    N = wq.shape[0]
+    if wq.shape[1] * 2 != K:
+        raise ValueError(f"gemm_w4a16: packed weight [{N}, {wq.shape[1]}] does not match K={K}")
+    w_scale = w_scale.to(torch.float16).contiguous()
+    w_zero = w_zero.to(torch.float16).contiguous()
+    bias, bdt = _bias(bias, N, x.device)
+    y = torch.empty(M, N, dtype=out_dtype or x.dtype, device=x.device)
+    _launch("gemm_w4a16", _native.lib().psq_gemm_w4a16, _p(x), _dt(x, "x"), x.stride(0), _p(wq), _p(w_scale), _p(w_zero),
+                                               int(group_size), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K,
+                                               _stream(x))
+    return y
+
+
+def gemm_w8a16(x, wq, w_scale, bias=None, out_dtype=None):
+    """int8 weight-only: y = round(fmaf(x @ q.T (fp32), w_scale[n], bias[n]))."""
+    _need_gpu(x, wq, w_scale)
+    x, wq = _rows2d(x), _rows2d(wq)
+    M, K = x.shape
+    N = wq.shape[0]
+    w_scale = w_scale.to(torch.float32).reshape(-1).contiguous()
+    bias, bdt = _bias(bias, N, x.device)
+    y = torch.empty(M, N, dtype=out_dtype or x.dtype, device=x.device)
+    _launch("gemm_w8a16", _native.lib().psq_gemm_w8a16, _p(x), _dt(x, "x"), x.stride(0), _p(wq), _p(w_scale), _p(bias), bdt,
+                                               _p(y), _dt(y, "out"), N, M, N, K, _stream(x))
+    return y
+
+
+# ------------------------------------------------------------------ dequantize
+def dequant_uint4(wq, w_scale, w_zero, group_size, out_dtype=torch.bfloat16):
+    _need_gpu(wq, w_scale, w_zero)
+    wq = wq.contiguous()
+    N, K = wq.shape[0], wq.shape[1] * 2
+    out = torch.empty(N, K, dtype=out_dtype, device=wq.device)
+    _launch("dequant_uint4", _native.lib().psq_dequant_uint4, _p(wq), _p(w_scale.to(torch.float16).contiguous()),
+                                                  _p(w_zero.to(torch.float16).contiguous()), int(group_size), N, K,
+                                                  _p(out), _dt(out, "out"), _stream(wq))
+    return out
+
+
+def dequant_i8_rows(q, w_scale, rot_group=0, out_dtype=torch.bfloat16):
+    _need_gpu(q, w_scale)
+    q = q.contiguous()
+    N, K = q.shape
+    out = torch.empty(N, K, dtype=out_dtype, device=q.device)
+    _launch("dequant_i8_rows", _native.lib().psq_dequant_i8_rows, _p(q), _p(w_scale.to(torch.float32).reshape(-1).contiguous()), N, K,
+                                                    int(rot_group or 0), _p(out), _dt(out, "out"), _stream(q))
+    return out
+
+
+def dequant_fp8(q, w_scale, out_dtype=torch.bfloat16):
+    _need_gpu(q)
+    q = q.contiguous()
+    N, K = q.shape
+    s = w_scale.to(device=q.device, dtype=torch.float32).reshape(-1).contiguous()
+    out = torch.empty(N, K, dtype=out_dtype, device=q.device)
+    _launch("dequant_fp8", _native.lib().psq_dequant_fp8, _p(q), _p(s), int(s.numel() > 1), N, K, _p(out), _dt(out, "out"),
+                                                _stream(q))
+    return out
+
+
+def device_supported(device):
+    device = torch.device(device)
+    if device.type != "cuda":
+        return False
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return bool(_native.lib().psq_device_supported(index))

@@ -1,0 +1,143 @@
+/*
+ * psquant.h -- C ABI of libpsquant.so, the MI355X (gfx950) quantized linear library.
+ *
+ * Plain pointers and sizes only; the caller (PyTorch) owns every buffer.  The library
+ * never allocates or frees device memory on these entry points.  Every launch goes to the
+ * caller's stream (`stream` is a hipStream_t passed as void*; NULL = the null stream).
+ * Every function returns 0 on success and a negative PSQ_E* code on failure, after which
+ * psq_last_error() returns a message for the calling thread.  Entry points are re-entrant
+ * and hold no per-call state.
+ *
+ * Reference interfaces replaced (ComfyUI-PowerShard 0.6.0):
+ *   - powershard/quant_linear.py:230-242 native_linear() -> comfy-kitchen ops
+ *     int8_linear / torch._scaled_mm / w4a8_int8_linear (NATIVE table, quant_linear.py:32-35)
+ *   - powershard/quant_linear.py:245-265 native_support()
+ *   - powershard/quant_linear.py:219-220 qt.dequantize() of the dequantize branch
+ *   - powershard/operations.py:84-93   dequantize_rows()
+ * Arithmetic conventions (bit-exact where stated) are those of the CPU oracle,
+ * oracle/psq_oracle.c, restated in the comments below.
+ */
+#ifndef PSQUANT_H
+#define PSQUANT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PSQ_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define PSQ_API __attribute__((visibility("default")))
+#else
+#define PSQ_API
+#endif
+
+/* element types of activations, bias and outputs */
+enum psq_dtype { PSQ_BF16 = 0, PSQ_F16 = 1, PSQ_F32 = 2 };
+
+/* error codes */
+enum psq_status {
+    PSQ_OK = 0,
+    PSQ_E_ARG = -1,         /* bad argument (null pointer, negative size, bad dtype) */
+    PSQ_E_SHAPE = -2,       /* shape/stride/alignment outside what the kernel supports */
+    PSQ_E_DEVICE = -3,      /* no gfx950 device current, or a HIP runtime error */
+    PSQ_E_LAUNCH = -4       /* kernel launch failed */
+};
+
+/* ABI version (PSQ_ABI_VERSION). */
+PSQ_API int psq_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none).  Never NULL. */
+PSQ_API const char *psq_last_error(void);
+
+/* 1 if HIP device `device` is a gfx950 (MI355X-class) GPU the kernels are built for, else 0.
+ * Replaces native_support()'s capability probe (powershard/quant_linear.py:245-265). */
+PSQ_API int psq_device_supported(int device);
+
+/* ---------------------------------------------------------------- activations
+ * Fused ConvRot rotation + per-row (token) absmax + quantize.  Replaces the activation
+ * side of comfy-kitchen's int8_linear / QuantizedTensor.from_float(rows, layout, scale)
+ * (powershard/quant_linear.py:233-236).
+ *   x      [M, K] bf16/f16 (x_dtype), row stride ldx elements, 16-byte aligned rows
+ *   rot_group  0 (no rotation) or a power of 4 in [4, 1024] dividing K: each group of
+ *          rot_group consecutive elements is multiplied by the regular Hadamard
+ *          H4^{(x)k}/sqrt(g) (powershard/operations.py:72-81) with the fixed-order fast
+ *          transform of the oracle.
+ *   static_scale  NULL for dynamic per-row scale, or a device pointer to one fp32 value
+ *          (the module's input_scale, powershard/quant_linear.py:28-30)
+ *   q      [M, K] int8 / e4m3fn codes, row stride ldq bytes
+ *   scale  [M] fp32 per-row scale (s = absmax/127 or absmax/448; 0 -> 1)
+ * K must be a multiple of 16 and at most 16384.  Bit-exact with the oracle. */
+PSQ_API int psq_quantize_rows_i8(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                         int rot_group, const float *static_scale, int8_t *q, int64_t ldq,
+                         float *scale, void *stream);
+PSQ_API int psq_quantize_rows_fp8(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                          int rot_group, const float *static_scale, uint8_t *q, int64_t ldq,
+                          float *scale, void *stream);
+
+/* ---------------------------------------------------------------------- GEMMs
+ * W8A8: y[m][n] = round_out(fmaf((float)acc, a_scale[m] * w_scale[n], bias[n])),
+ * acc = sum_k a[m][k] * w[n][k] in int32.  Replaces comfy-kitchen int8_linear behind
+ * F.linear(QuantizedTensor, QuantizedTensor, bias) (powershard/quant_linear.py:236-237).
+ *   a [M, K] int8 (lda), w [N, K] int8 (ldw), a_scale [M] fp32, w_scale [N] fp32,
+ *   bias [N] (bias_dtype) or NULL, y [M, N] (y_dtype, ldy elements).
+ * K % 128 == 0; lda, ldw multiples of 16; 16-byte aligned a, w. */
+PSQ_API int psq_gemm_i8(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w,
+                int64_t ldw, const float *w_scale, const void *bias, int bias_dtype, void *y,
+                int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* Same GEMM, raw int32 accumulators c[m][n] (ldc elements); for bit-exact checking. */
+PSQ_API int psq_gemm_i8_i32(const int8_t *a, int64_t lda, const int8_t *w, int64_t ldw, int32_t *c,
+                    int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* FP8 e4m3fn x e4m3fn -> fp32 accumulate on the gfx950 f8f6f4 MFMA, same epilogue.
+ * w_scale is one fp32 (w_scale_per_row = 0) or [N] (1).  Replaces torch._scaled_mm for
+ * float8_e4m3fn (powershard/quant_linear.py:32, 236-237). */
+PSQ_API int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, const uint8_t *w,
+                 int64_t ldw, const float *w_scale, int w_scale_per_row, const void *bias,
+                 int bias_dtype, void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
+                 int64_t K, void *stream);
+
+/* W4A16: uint4 asymmetric group weights dequantized in registers,
+ * w = round_bf16((float(q) - float(zero)) * float(scale)), multiplied on bf16 MFMA with
+ * fp32 accumulation; y = round_out(acc + bias).  Replaces the int4 F.linear dispatch
+ * (powershard/quant_linear.py:239, weight-only formats) and matches the dequantize
+ * branch F.linear(rows, qt.dequantize().to(bf16), bias) (quant_linear.py:219-220).
+ *   x [M, K] bf16 (ldx), wq [N, K/2] bytes (low nibble = even k), scale/zero [N, K/group]
+ *   fp16, group_size in {32, 64, 128, 256, ...} multiple of 32 dividing K. */
+PSQ_API int psq_gemm_w4a16(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq,
+                   const uint16_t *w_scale, const uint16_t *w_zero, int group_size,
+                   const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,
+                   int64_t M, int64_t N, int64_t K, void *stream);
+
+/* W8A16 (int8 weight-only, per-row fp32 scale): y = round_out(fmaf(sum x*q, w_scale[n],
+ * bias[n])), x bf16, q exact in bf16.  Int8 weight-only linear of
+ * powershard/operations.py:96-132 (Int8Linear, non-ConvRot storage). */
+PSQ_API int psq_gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t *wq,
+                   const float *w_scale, const void *bias, int bias_dtype, void *y,
+                   int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* ---------------------------------------------------------------- dequantize
+ * GPU implementations of QuantizedTensor.dequantize() for the dequantize compute mode
+ * (powershard/quant_linear.py:216-220) and of dequantize_rows (operations.py:84-93). */
+
+/* out[n][k] = round_out((float(q) - float(zero)) * float(scale)), uint4 layout as above. */
+PSQ_API int psq_dequant_uint4(const uint8_t *wq, const uint16_t *w_scale, const uint16_t *w_zero,
+                      int group_size, int64_t N, int64_t K, void *out, int out_dtype,
+                      void *stream);
+
+/* out = round_out((float)q * scale[n]) then, when rot_group > 0, each group of rot_group
+ * values multiplied by H^T (= H) with the oracle's fixed-order fast transform, in fp32. */
+PSQ_API int psq_dequant_i8_rows(const int8_t *q, const float *w_scale, int64_t N, int64_t K,
+                        int rot_group, void *out, int out_dtype, void *stream);
+
+/* out = round_out(e4m3_to_f32(q) * scale[n or 0]). */
+PSQ_API int psq_dequant_fp8(const uint8_t *q, const float *w_scale, int w_scale_per_row, int64_t N,
+                    int64_t K, void *out, int out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PSQUANT_H */
