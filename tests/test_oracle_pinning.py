@@ -169,7 +169,7 @@ def test_bf16_and_f16_encoders_vs_library_casts():
     got_b = torch.tensor([oracle.lib().psq_or_f32_to_bf16(float(v)) for v in x], dtype=torch.int32)
     ref_b = x.to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
     assert torch.equal(got_b, ref_b)
-    xs = x[x.abs() < 1e6]
+    xs = x[x.abs() < 6e4]
     got_h = np.array([oracle.lib().psq_or_f32_to_f16(float(v)) for v in xs], dtype=np.uint16)
     ref_h = xs.numpy().astype(np.float16).view(np.uint16)
     assert np.array_equal(got_h, ref_h)
