@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample time")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain elementwise copy of 1 GiB (3 launches), the reference point that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     return ap.parse_args()
 
 
@@ -313,6 +316,16 @@ def main():
         sys.exit(2)
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.calibrate_copy:
+        n = 1 << 28   # 2^28 fp32 = 1 GiB read and 1 GiB written per launch
+        x = torch.ones(n, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.neg(x, out=y)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "torch.neg fp32 elementwise", "bytes_read_per_launch": 4 * n,
+                          "bytes_written_per_launch": 4 * n, "launches": 3}))
+        return
     from powershard_amd import _native
     _native.lib()
     h, sample = headline(args)
