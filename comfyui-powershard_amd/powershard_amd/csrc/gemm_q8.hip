@@ -18,14 +18,25 @@
 namespace psq {
 namespace {
 
+// Tuning knobs (compile-time): ring depth and the int8 LDS swizzle.
+#ifndef PSQ_Q8_NSTAGE
+#define PSQ_Q8_NSTAGE 4
+#endif
+#ifndef PSQ_Q8_SWZ
+#define PSQ_Q8_SWZ 1
+#endif
+#ifndef PSQ_Q8_GROUP_M
+#define PSQ_Q8_GROUP_M 8
+#endif
+
 constexpr int BM = 256, BN = 256, BK = 64;    // BK in bytes (= elements for int8/fp8)
-constexpr int NSTAGE = 4;                      // LDS ring depth: 3 stages in flight
+constexpr int NSTAGE = PSQ_Q8_NSTAGE;          // LDS ring depth: NSTAGE - 1 stages in flight
 constexpr int NTHREADS = 256;                  // 4 waves, one per SIMD
 constexpr int WAVE_M = 128, WAVE_N = 128;
 constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;   // 4 x 4 MFMA tiles of 32 x 32 per wave
 constexpr int STAGE_BYTES = BM * BK;                 // one operand, one stage (16 KB)
 constexpr int LOADS = (BM * BK / 1024) / (NTHREADS / 64);   // 1 KB wave loads per operand per stage (4)
-constexpr int GROUP_M = 8;
+constexpr int GROUP_M = PSQ_Q8_GROUP_M;
 
 enum { OUT_BF16 = PSQ_BF16, OUT_F16 = PSQ_F16, OUT_F32 = PSQ_F32, OUT_I32 = 3 };
 
@@ -46,29 +57,56 @@ __device__ __forceinline__ void store4(void *y, int64_t off, const float (&v)[4]
 {
     if constexpr (OUT == OUT_F32) {
         float *p = (float *)y + off;
-        if (vec) *(v4f *)p = v4f{v[0], v[1], v[2], v[3]};
-        else for (int c = 0; c < 4 && c < n_left; c++) p[c] = v[c];
+        if (vec) {
+            *(v4f *)p = v4f{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if (c < n_left) p[c] = v[c];
+        }
     } else {
         uint16_t *p = (uint16_t *)y + off;
         uint32_t h[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) h[c] = f32_to_half<OUT>(v[c]);
-        if (vec) *(v2i *)p = v2i{(int)(h[0] | (h[1] << 16)), (int)(h[2] | (h[3] << 16))};
-        else for (int c = 0; c < 4 && c < n_left; c++) p[c] = (uint16_t)h[c];
+        if (vec) {
+            *(v2i *)p = v2i{(int)(h[0] | (h[1] << 16)), (int)(h[2] | (h[3] << 16))};
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if (c < n_left) p[c] = (uint16_t)h[c];
+        }
     }
 }
+
+// LDS: the K-loop ring, reused by the epilogue as four 32 KB per-wave staging areas, then the
+// tile's row scales, column scales and biases.
+constexpr size_t kRingBytes = (NSTAGE * 2 * STAGE_BYTES) > 131072 ? (NSTAGE * 2 * STAGE_BYTES) : 131072;
 
 typedef __attribute__((address_space(3))) uint8_t *lds_ptr;
 typedef const __attribute__((address_space(1))) void *glb_ptr;
 
-// Stage rows are 64 bytes = four 16-byte chunks.  int8 stores chunk ^ ((row >> 1) & 3): the eight
-// rows read together by a ds_read_b128 quarter-wave then cover all 32 banks once.  fp8 reads 32
-// bytes (two chunks) per lane, so it swaps whole 32-byte halves, chunk ^ (((row >> 1) & 1) << 1),
-// which keeps each lane's fragment contiguous and in k order.
+// Stage rows are 64 bytes = four 16-byte chunks; a 32-lane MFMA fragment read touches 32
+// consecutive rows at one logical chunk.  int8 stores chunk ^ x(row) with x = (r1 ^ r3, r2) (bits
+// of the row): bijective in (r1, r2) and in (r2, r3), so both 8 consecutive rows (a 32-bank,
+// 128-byte LDS cycle) and 16 consecutive rows (a 64-bank, 256-byte cycle) hit distinct banks.
+// fp8 reads 32 bytes (two chunks) per lane, so it swaps whole 32-byte halves,
+// chunk ^ (((row >> 1) & 1) << 1), which keeps each lane's fragment contiguous and in k order.
+__device__ __forceinline__ int swz_i8(int r)
+{
+#if PSQ_Q8_SWZ == 0
+    return (r >> 1) & 3;
+#elif PSQ_Q8_SWZ == 1
+    return (((r >> 1) ^ (r >> 3)) & 1) | (r & 4) >> 1;
+#else
+    return (r >> 2) & 3;
+#endif
+}
+
 template <bool FP8>
 __device__ __forceinline__ int swz(int row, int chunk)
 {
-    const int x = FP8 ? (((row >> 1) & 1) << 1) : ((row >> 1) & 3);
+    const int x = FP8 ? (((row >> 1) & 1) << 1) : swz_i8(row);
     return row * BK + ((chunk ^ x) << 4);
 }
 
@@ -77,6 +115,36 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt()
 {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the K loop.  __syncthreads() carries a workgroup fence, which makes the
+// compiler drain every outstanding global->LDS load (vmcnt(0)) -- including the stages just put
+// in flight.  The loop instead waits explicitly for the stage it needs (wait_vmcnt) and for its
+// own LDS reads (lgkmcnt(0)), then meets the other waves; the asm memory clobber keeps the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void stage_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Scheduling hints (masks: 0x008 MFMA, 0x020 VMEM read, 0x100 DS read).  With one wave per
+// SIMD every issue slot not spent on an MFMA idles the matrix core, so the global->LDS loads of a
+// refill and the LDS fragment reads of the next k-step are each slotted behind an MFMA: the loads
+// first (they follow only reads the first MFMA already waited for), then the reads.
+template <int N_VMEM, int N_DS, int N_MFMA>
+__device__ __forceinline__ void interleave_with_mfma()
+{
+    static_assert(N_VMEM + N_DS <= N_MFMA, "one memory instruction per MFMA at most");
+#pragma unroll
+    for (int i = 0; i < N_VMEM; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < N_DS; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, (N_MFMA - N_VMEM) / N_DS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
 }
 
 template <bool FP8> struct Frag;
@@ -102,6 +170,16 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     tile_order(blockIdx.x, nbm, nbn, GROUP_M, pm, pn);
     const int m0 = pm * BM, n0 = pn * BN;
 
+    // The tile's epilogue operands (256 row scales, 256 column scales, 256 biases) go to LDS past
+    // the ring before the loads of the K loop, so the epilogue reads them without memory latency.
+    float *s_as = (float *)(smem + kRingBytes), *s_ws = s_as + BM, *s_b = s_ws + BN;
+    if constexpr (OUT != OUT_I32) {
+        s_as[tid] = ep.a_scale[min(m0 + tid, M - 1)];
+        const int nc = min(n0 + tid, N - 1);
+        s_ws[tid] = ep.w_scale[ep.w_per_row ? nc : 0];
+        s_b[tid] = ep.bias ? load_elem(ep.bias, nc, ep.bias_dtype) : 0.0f;
+    }
+
     // global -> LDS: a wave load moves 1 KB = 16 rows x 4 chunks; lane L fills physical slot L of
     // the block (row 16 b + L / 4, physical chunk L % 4) and reads the logical chunk stored there.
     const uint8_t *pa[LOADS];
@@ -110,7 +188,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     for (int j = 0; j < LOADS; j++) {
         const int b = j * (NTHREADS / 64) + wave;
         const int r = 16 * b + (lane >> 2);
-        const int c = (lane & 3) ^ (FP8 ? (((r >> 1) & 1) << 1) : ((r >> 1) & 3));
+        const int c = (lane & 3) ^ (FP8 ? (((r >> 1) & 1) << 1) : swz_i8(r));
         pa[j] = A + (int64_t)min(m0 + r, M - 1) * lda + c * 16;
         pw[j] = W + (int64_t)min(n0 + r, N - 1) * ldw + c * 16;
     }
@@ -169,11 +247,11 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     const int nk = K / BK;
     // Prologue: stages 0 .. NSTAGE-2 in flight.  Every step below issues exactly one stage (clamped
     // to the last one, re-loading it into a ring slot nobody reads again), so the number of loads
-    // younger than the stage being waited for is always 2 LPS and the waits carry no branches.
+    // younger than the stage being waited for is always (NSTAGE - 2) LPS: the waits carry no branches.
 #pragma unroll
     for (int s = 0; s < NSTAGE - 1; s++) issue_stage(min(s, nk - 1), s);
-    wait_vmcnt<2 * LPS>();
-    __syncthreads();
+    wait_vmcnt<(NSTAGE - 2) * LPS>();
+    stage_barrier();
 
     // One MFMA k-step g = KS * kt + ks: at the first k-step of stage kt refill the ring slot last
     // read in stage kt - 1 (every wave passed the barrier that ended it); prefetch the fragments of
@@ -186,11 +264,13 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         if (ks + 1 < KS) {
             read_frags(kt, ks + 1, na, nw);
         } else {
-            wait_vmcnt<2 * LPS>();   // stage kt + 1 landed for this wave ...
-            __syncthreads();         // ... and for every wave
+            wait_vmcnt<(NSTAGE - 2) * LPS>();   // stage kt + 1 landed for this wave ...
+            stage_barrier();         // ... and for every wave
             read_frags(min(kt + 1, nk - 1), 0, na, nw);
         }
         mfma(acc, ca, cw);
+        if (ks == 0) interleave_with_mfma<LPS, TM + TN, TM * TN>();
+        else interleave_with_mfma<0, TM + TN, TM * TN>();
     };
     FT fa0[TM], fw0[TN], fa1[TM], fw1[TN];
     if constexpr (FP8) {
@@ -201,8 +281,16 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             issue_stage(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
             read_frags(kt, 0, fa0, fw0);
             mfma(acc, fa0, fw0);
-            wait_vmcnt<2 * LPS>();
-            __syncthreads();
+            // reads first (the MFMAs consume them in issue order), then one refill load per MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+#pragma unroll
+            for (int i = 0; i < LPS; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - LPS, 0);
+            wait_vmcnt<(NSTAGE - 2) * LPS>();
+            stage_barrier();
         }
     } else {
         read_frags(0, 0, fa0, fw0);
@@ -228,9 +316,8 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     float ws[4], bs[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        const int nc = min(nb + c, N - 1);
-        ws[c] = (OUT == OUT_I32) ? 1.0f : ep.w_scale[ep.w_per_row ? nc : 0];
-        bs[c] = (OUT != OUT_I32 && ep.bias) ? load_elem(ep.bias, nc, ep.bias_dtype) : 0.0f;
+        ws[c] = (OUT == OUT_I32) ? 1.0f : s_ws[wn * WAVE_N + col4 + c];
+        bs[c] = (OUT == OUT_I32) ? 0.0f : s_b[wn * WAVE_N + col4 + c];
     }
 #pragma unroll
     for (int h = 0; h < 2; h++) {
@@ -243,7 +330,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                     const int row = il * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                     const Acc &a = acc[2 * h + il][j];
                     float v;
-                    if constexpr (OUT == OUT_I32 || !FP8) v = __builtin_bit_cast(float, (int)a[r]);
+                    if constexpr (OUT == OUT_I32 || !FP8) v = __int_as_float((int)a[r]);
                     else v = a[r];
                     stage[row * 128 + j * 32 + (lane & 31)] = v;
                 }
@@ -251,22 +338,26 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         for (int st = 0; st < 32; st++) {
             const int row = 2 * st + (lane >> 5);
             const v4f raw = *(const v4f *)(stage + row * 128 + col4);
+            // whole-vector reinterpretation only: hipcc mis-lowers __builtin_bit_cast applied to a
+            // single ext_vector element (it reads element 0)
+            const v4i rawi = __builtin_bit_cast(v4i, raw);
             const int m = m0 + wm * WAVE_M + h * 64 + row;
             if (m >= M) continue;
             if constexpr (OUT == OUT_I32) {
                 int32_t *C = (int32_t *)ep.y + (int64_t)m * ep.ldy + nb;
                 if (ep.vec && nb + 3 < N) {
-                    *(v4i *)C = __builtin_bit_cast(v4i, raw);
+                    *(v4i *)C = rawi;
                 } else {
+#pragma unroll
                     for (int c = 0; c < 4; c++)
-                        if (nb + c < N) C[c] = __builtin_bit_cast(int, raw[c]);
+                        if (nb + c < N) C[c] = rawi[c];
                 }
             } else {
-                const float as = ep.a_scale[m];
+                const float as = s_as[wm * WAVE_M + h * 64 + row];
                 float y[4];
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    const float accv = FP8 ? raw[c] : (float)__builtin_bit_cast(int, raw[c]);
+                    const float accv = FP8 ? raw[c] : (float)rawi[c];
                     y[c] = __builtin_fmaf(accv, as * ws[c], bs[c]);
                 }
                 store4<OUT>(ep.y, (int64_t)m * ep.ldy + nb, y, ep.vec && nb + 3 < N, N - nb);
@@ -275,7 +366,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     }
 }
 
-constexpr size_t kSmemBytes = NSTAGE * 2 * STAGE_BYTES;   // 128 KB
+constexpr size_t kSmemBytes = kRingBytes + 3 * 256 * sizeof(float);   // ring (>= the 128 KB epilogue stage) + scales
 
 template <bool FP8, int OUT>
 int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N, int64_t K,

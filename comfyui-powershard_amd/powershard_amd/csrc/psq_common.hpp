@@ -51,9 +51,17 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h16)
     return (float)h;
 }
 
+// Forces `x` to be materialized as an fp32 value: the backend otherwise folds an fma or mul
+// feeding an f16 conversion into v_fma_mix / v_mad_mix, rounding once instead of twice.
+__device__ __forceinline__ float opaque(float x)
+{
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 __device__ __forceinline__ uint32_t f32_to_f16(float f)
 {
-    _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+    _Float16 h = (_Float16)opaque(f);  // v_cvt_f16_f32, round to nearest even
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 

@@ -154,7 +154,7 @@ def test_gemm_i8_i32_bitexact(gpu, M, N, K):
     assert_bitexact(c, oracle.gemm_i8_i32(a, w), "int32 acc")
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1000, 520, 5120), (257, 264, 256)])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1000, 520, 5120), (257, 264, 256), (130, 777, 384), (70, 100, 256)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_gemm_i8_epilogue(gpu, M, N, K, out_dtype, with_bias):
@@ -173,7 +173,7 @@ def test_gemm_i8_epilogue(gpu, M, N, K, out_dtype, with_bias):
 
 
 # ---------------------------------------------------------------------------- fp8
-@pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1000, 520, 5120), (17, 33, 128)])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1000, 520, 5120), (17, 33, 128), (129, 777, 1024)])
 @pytest.mark.parametrize("per_row", [False, True])
 def test_gemm_fp8(gpu, M, N, K, per_row):
     from powershard_amd import ops
