@@ -6,22 +6,21 @@
 //   int8: acc = sum_k a[m][k] w[n][k] in int32 (v_mfma_i32_32x32x32_i8, exact)
 //   fp8 : acc = the same in fp32 (v_mfma_f32_32x32x64_f8f6f4, e4m3 x e4m3)
 //
-// Tiling (MI355X-first): a 256 x 256 output tile per workgroup of 4 waves, one per SIMD (2 x 2,
-// each wave 128 x 128 = 4 x 4 MFMA tiles of 32 x 32, accumulators in the AGPR half of the
-// register file).  K runs in stages of 64 bytes through a 4-deep LDS ring (4 x 32 KB) filled by
-// direct global->LDS loads (global_load_lds_dwordx4: no staging registers, no LDS write
-// instructions), three stages in flight.  Fragments are double-buffered in registers so the
-// LDS reads of the next k-step overlap the MFMAs of the current one; one barrier per stage.  Workgroups are renumbered so each XCD owns a contiguous, L2-friendly
-// group of tiles.  MFMA-bound: 2 M N K ops per launch.
+// Tiling (MI355X-first): a persistent grid of one workgroup per CU walks 256 x 256 output tiles;
+// a workgroup is 4 waves, one per SIMD (2 x 2, each wave 128 x 128 = 4 x 4 MFMA tiles of 32 x 32,
+// accumulators in the AGPR half of the register file).  K runs in stages of 64 bytes through a
+// 4-deep LDS ring (4 x 32 KB) filled by direct global->LDS loads (global_load_lds_dwordx4: no
+// staging registers, no LDS write instructions), three stages in flight, continuously across the
+// tiles of a workgroup.  Fragments are double-buffered in registers so the LDS reads of the next
+// k-step overlap the MFMAs of the current one; one barrier per stage.  The epilogue converts the
+// accumulators in registers and stores them without an LDS round trip while the next tile's first
+// stages load.  MFMA-bound: 2 M N K ops per launch.
 #include "psq_common.hpp"
 
 namespace psq {
 namespace {
 
-// Tuning knobs (compile-time): ring depth and the int8 LDS swizzle.
-#ifndef PSQ_Q8_NSTAGE
-#define PSQ_Q8_NSTAGE 4
-#endif
+// Tuning knobs (compile-time): the int8 LDS swizzle and the tile grouping.
 #ifndef PSQ_Q8_SWZ
 #define PSQ_Q8_SWZ 1
 #endif
@@ -30,7 +29,9 @@ namespace {
 #endif
 
 constexpr int BM = 256, BN = 256, BK = 64;    // BK in bytes (= elements for int8/fp8)
-constexpr int NSTAGE = PSQ_Q8_NSTAGE;          // LDS ring depth: NSTAGE - 1 stages in flight
+// LDS ring depth (NSTAGE - 1 stages in flight): 4 for int8; 3 for fp8, whose fragment sets
+// alternate per stage and so need an even number of stages between tile switches.
+template <bool FP8> constexpr int ring_depth() { return FP8 ? 3 : 4; }
 constexpr int NTHREADS = 256;                  // 4 waves, one per SIMD
 constexpr int WAVE_M = 128, WAVE_N = 128;
 constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;   // 4 x 4 MFMA tiles of 32 x 32 per wave
@@ -51,37 +52,35 @@ struct Epi {
     int vec;          // rows of y are 16-byte aligned: 4-element vector stores allowed
 };
 
-// Store 4 consecutive outputs (RNE to bf16 / f16, or fp32); `n_left` bounds a partial group.
+// Four consecutive outputs packed for one vector store: 2 words of bf16 / f16 (round to nearest
+// even), or 4 words of fp32 / int32 bits.
+#ifndef PSQ_NATIVE_BF16
+#define PSQ_NATIVE_BF16 1
+#endif
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 template <int OUT>
-__device__ __forceinline__ void store4(void *y, int64_t off, const float (&v)[4], bool vec, int n_left)
+__device__ __forceinline__ uint32_t pack2(float a, float b)
 {
-    if constexpr (OUT == OUT_F32) {
-        float *p = (float *)y + off;
-        if (vec) {
-            *(v4f *)p = v4f{v[0], v[1], v[2], v[3]};
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                if (c < n_left) p[c] = v[c];
-        }
+    if constexpr (OUT == OUT_BF16 && PSQ_NATIVE_BF16) {
+        // v_cvt_pk_bf16_f32: round to nearest even, as f32_to_bf16 (NaN inputs give a quiet NaN)
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
     } else {
-        uint16_t *p = (uint16_t *)y + off;
-        uint32_t h[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) h[c] = f32_to_half<OUT>(v[c]);
-        if (vec) {
-            *(v2i *)p = v2i{(int)(h[0] | (h[1] << 16)), (int)(h[2] | (h[3] << 16))};
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                if (c < n_left) p[c] = (uint16_t)h[c];
-        }
+        return f32_to_half<OUT>(a) | (f32_to_half<OUT>(b) << 16);
     }
 }
 
-// LDS: the K-loop ring, reused by the epilogue as four 32 KB per-wave staging areas, then the
-// tile's row scales, column scales and biases.
-constexpr size_t kRingBytes = (NSTAGE * 2 * STAGE_BYTES) > 131072 ? (NSTAGE * 2 * STAGE_BYTES) : 131072;
+// One output element (the slow path of partial tiles and unaligned outputs).
+template <int OUT>
+__device__ __forceinline__ void store1(void *p, int c, float v)
+{
+    if constexpr (OUT == OUT_F32) ((float *)p)[c] = v;
+    else ((uint16_t *)p)[c] = (uint16_t)f32_to_half<OUT>(v);
+}
+
+// LDS: the K-loop ring, then the epilogue operands.
+constexpr size_t kRingBytes = 4 * 2 * STAGE_BYTES;   // the deeper (int8) ring
 
 typedef __attribute__((address_space(3))) uint8_t *lds_ptr;
 typedef const __attribute__((address_space(1))) void *glb_ptr;
@@ -151,64 +150,143 @@ template <bool FP8> struct Frag;
 template <> struct Frag<false> { typedef v4i T; static constexpr int KSTEP = 32; };   // 32x32x32 i8
 template <> struct Frag<true> { typedef v8i T; static constexpr int KSTEP = 64; };    // 32x32x64 f8f6f4
 
+// Epilogue operands of a tile in LDS past the ring: row scales, column scales and raw bias words
+// (one 32-bit word per column: the bias element zero-extended, or the fp32 bits), three buffers
+// used round-robin by consecutive tiles of a workgroup.
+constexpr int NSCALEBUF = 3;
+constexpr int SCALE_WORDS = BM + 2 * BN;
+constexpr size_t kSmemBytes = kRingBytes + NSCALEBUF * SCALE_WORDS * sizeof(float);
+
+// Tiles of a persistent workgroup.  Hardware dispatches workgroup b to XCD b % 8; the tile
+// sequence (grouped raster order, GROUP_M row tiles per group) is cut into one contiguous chunk
+// per XCD, sized by its number of workgroups, and a workgroup takes every wx-th tile of its XCD's
+// chunk.  The workgroups of one XCD therefore work on GROUP_M x (wx / GROUP_M) neighbouring tiles
+// at a time and share their A and W rows in that XCD's L2.
+__device__ __forceinline__ void tile_range(int b, int G, int T, int &v, int &step, int &end)
+{
+    const int x = b & 7, slot = b >> 3;
+    int pre = 0;
+    for (int y = 0; y < x; y++) pre += (G - y + 7) >> 3;
+    const int wx = (G - x + 7) >> 3;
+    v = (int)((int64_t)T * pre / G) + slot;
+    step = wx;
+    end = (int)((int64_t)T * (pre + wx) / G);
+}
+
+__device__ __forceinline__ void tile_coords(int v, int nbm, int nbn, int &m0, int &n0)
+{
+    const int per_group = GROUP_M * nbn;
+    const int g = v / per_group, first = g * GROUP_M;
+    const int h = min(nbm - first, GROUP_M);
+    const int r = v - g * per_group;
+    m0 = (first + r % h) * BM;
+    n0 = (r / h) * BN;
+}
+
+// Reads an accumulator element through an AGPR operand.  The epilogue's arithmetic cannot take
+// AGPRs, and left to itself the register allocator then keeps the whole accumulator array in
+// VGPRs (and spills everything else); reading each element with an explicit AGPR-to-VGPR move
+// keeps the accumulators in the AGPR file for the MFMAs.
+__device__ __forceinline__ int agpr_read(int a)
+{
+    int v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+__device__ __forceinline__ int agpr_read(float a)
+{
+    int v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+
+// Bias word (see above) to fp32.
+__device__ __forceinline__ float bias_word(uint32_t w, int dt)
+{
+    if (dt == PSQ_BF16) return __uint_as_float(w << 16);
+    if (dt == PSQ_F16) return f16_to_f32(w);
+    return __uint_as_float(w);
+}
+
+// Persistent kernel: one workgroup per CU walks its tiles; the LDS ring streams continuously
+// across tile boundaries, so the first stages of the next tile load while the current tile's
+// epilogue runs.  The MFMAs compute the transposed tile (W fragment as the first operand), which
+// gives each lane one output row and, per 32 x 32 tile, four runs of 4 consecutive columns: the
+// epilogue converts the accumulators in registers and stores them directly.
 template <bool FP8, int OUT>
 __global__ void __launch_bounds__(NTHREADS, 1)
 gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W, int64_t ldw,
                int M, int N, int K, Epi ep)
 {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];   // [NSTAGE][A | W]
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];   // ring [NSTAGE][A | W], scales
     using Acc = typename std::conditional<FP8, v16f, v16i>::type;
     using FT = typename Frag<FP8>::T;
-    constexpr int KSTEP = Frag<FP8>::KSTEP;
-    constexpr int KS = BK / KSTEP;                 // MFMA k-steps per stage (2 for int8, 1 for fp8)
-    constexpr int LPS = 2 * LOADS;                 // DMA instructions per wave per stage
+    static_assert(BK / Frag<FP8>::KSTEP == (FP8 ? 1 : 2), "k-steps per stage: 2 for int8, 1 for fp8");
+    constexpr int LPS = 2 * LOADS;                 // ring DMA instructions per wave per stage
+    constexpr bool SCALED = OUT != OUT_I32;
+    constexpr int NSTAGE = ring_depth<FP8>();
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
-    int pm, pn;
-    tile_order(blockIdx.x, nbm, nbn, GROUP_M, pm, pn);
-    const int m0 = pm * BM, n0 = pn * BN;
+    int v, step, vend;
+    tile_range(blockIdx.x, gridDim.x, nbm * nbn, v, step, vend);
+    if (v >= vend) return;
+    const int nk = K / BK;
+    uint32_t *const scale_lds = (uint32_t *)(smem + kRingBytes);
 
-    // The tile's epilogue operands (256 row scales, 256 column scales, 256 biases) go to LDS past
-    // the ring before the loads of the K loop, so the epilogue reads them without memory latency.
-    float *s_as = (float *)(smem + kRingBytes), *s_ws = s_as + BM, *s_b = s_ws + BN;
-    if constexpr (OUT != OUT_I32) {
-        s_as[tid] = ep.a_scale[min(m0 + tid, M - 1)];
-        const int nc = min(n0 + tid, N - 1);
-        s_ws[tid] = ep.w_scale[ep.w_per_row ? nc : 0];
-        s_b[tid] = ep.bias ? load_elem(ep.bias, nc, ep.bias_dtype) : 0.0f;
-    }
-
+    // ---------------------------------------------------------------- ring loads
     // global -> LDS: a wave load moves 1 KB = 16 rows x 4 chunks; lane L fills physical slot L of
     // the block (row 16 b + L / 4, physical chunk L % 4) and reads the logical chunk stored there.
-    const uint8_t *pa[LOADS];
-    const uint8_t *pw[LOADS];
+    // The loads run NSTAGE - 1 stages ahead of the computation: during the last NSTAGE - 1 stages
+    // of a tile they fetch the first stages of the workgroup's next tile (pointer set `nx`); after
+    // its last tile a workgroup re-issues the tile's last stage, a load into a ring slot nobody
+    // reads again, so every stage issues the same number of loads and the waits are static.
+    struct Ptrs { const uint8_t *a[LOADS], *w[LOADS]; };
+    Ptrs cu, nx;
+    auto point_at = [&](int tv, int buf, Ptrs &p) {
+        int m0, n0;
+        tile_coords(tv, nbm, nbn, m0, n0);
 #pragma unroll
-    for (int j = 0; j < LOADS; j++) {
-        const int b = j * (NTHREADS / 64) + wave;
-        const int r = 16 * b + (lane >> 2);
-        const int c = (lane & 3) ^ (FP8 ? (((r >> 1) & 1) << 1) : swz_i8(r));
-        pa[j] = A + (int64_t)min(m0 + r, M - 1) * lda + c * 16;
-        pw[j] = W + (int64_t)min(n0 + r, N - 1) * ldw + c * 16;
-    }
-    auto issue_stage = [&](int kt, int slot) {
-        const int64_t koff = (int64_t)kt * BK;
+        for (int j = 0; j < LOADS; j++) {
+            const int b = j * (NTHREADS / 64) + wave;
+            const int r = 16 * b + (lane >> 2);
+            const int c = (lane & 3) ^ (FP8 ? (((r >> 1) & 1) << 1) : swz_i8(r));
+            p.a[j] = A + (int64_t)min(m0 + r, M - 1) * lda + c * 16;
+            p.w[j] = W + (int64_t)min(n0 + r, N - 1) * ldw + c * 16;
+        }
+        if constexpr (SCALED) {
+            // the tile's row scales, column scales and bias words: 64 entries of each per wave
+            lds_ptr dst = (lds_ptr)(scale_lds + buf * SCALE_WORDS + 64 * wave);
+            const int m = min(m0 + 64 * wave + lane, M - 1), n = min(n0 + 64 * wave + lane, N - 1);
+            __builtin_amdgcn_global_load_lds((glb_ptr)(ep.a_scale + m), dst, 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr)(ep.w_scale + (ep.w_per_row ? n : 0)), dst + 4 * BM, 4, 0, 0);
+            if (ep.bias) {
+                const uint8_t *bp = (const uint8_t *)ep.bias + (int64_t)n * (ep.bias_dtype == PSQ_F32 ? 4 : 2);
+                if (ep.bias_dtype == PSQ_F32) __builtin_amdgcn_global_load_lds((glb_ptr)bp, dst + 4 * (BM + BN), 4, 0, 0);
+                else __builtin_amdgcn_global_load_lds((glb_ptr)bp, dst + 4 * (BM + BN), 2, 0, 0);
+            }
+        }
+    };
+    // load stage `koff` of the current tile (same) or of the next one into ring slot `slot`
+    auto issue_stage = [&](int slot, bool same, int64_t koff) {
         lds_ptr dA = (lds_ptr)(smem + slot * 2 * STAGE_BYTES);
 #pragma unroll
         for (int j = 0; j < LOADS; j++) {
             const int b = j * (NTHREADS / 64) + wave;
-            __builtin_amdgcn_global_load_lds((glb_ptr)(pa[j] + koff), dA + 1024 * b, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((glb_ptr)(pw[j] + koff), dA + STAGE_BYTES + 1024 * b, 16, 0, 0);
+            const uint8_t *ga = (same ? cu.a[j] : nx.a[j]) + koff;
+            const uint8_t *gw = (same ? cu.w[j] : nx.w[j]) + koff;
+            __builtin_amdgcn_global_load_lds((glb_ptr)ga, dA + 1024 * b, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr)gw, dA + STAGE_BYTES + 1024 * b, 16, 0, 0);
         }
     };
 
-    // MFMA operand layout (32 x 32 tiles): lane holds row (lane & 31) of A / of W and the k-slice
-    // (lane >> 5) of the instruction's K; A and W use the same slice, so the dot products are
+    // MFMA operand layout (32 x 32 tiles): lane holds row (lane & 31) of W / of A and the k-slice
+    // (lane >> 5) of the instruction's K; both operands use the same slice, so the dot products are
     // complete whatever order the hardware sums a slice in.
     const int frow = lane & 31, fk = lane >> 5;
-    auto read_frags = [&](int kt, int ks, FT (&fa)[TM], FT (&fw)[TN]) {
-        const uint8_t *sA = smem + (kt % NSTAGE) * 2 * STAGE_BYTES;
+    auto read_frags = [&](int slot, int ks, FT (&fa)[TM], FT (&fw)[TN]) {
+        const uint8_t *sA = smem + slot * 2 * STAGE_BYTES;
         const uint8_t *sW = sA + STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < TM; i++) {
@@ -223,150 +301,220 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             else fw[j] = *(const v4i *)(sW + swz<false>(r, 2 * ks + fk));
         }
     };
-    auto mfma = [&](Acc (&acc)[TM][TN], const FT (&fa)[TM], const FT (&fw)[TN]) {
+    // acc[i][j] is the transposed 32 x 32 tile: W rows (output columns) x A rows (output rows).
+    // ZERO starts a tile: the accumulator input is the constant 0.
+    Acc acc[TM][TN];
+    auto mfma = [&](auto zero, int i0, int i1, const FT (&fa)[TM], const FT (&fw)[TN]) {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int i = i0; i < i1; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
+                const Acc c = decltype(zero)::value ? Acc{} : acc[i][j];
                 if constexpr (FP8)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fw[j], acc[i][j], 0, 0, 0, 127,
-                                                                               0, 127);
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], c, 0, 0, 0, 127, 0, 127);
                 else
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fw[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], c, 0, 0, 0);
             }
     };
 
-    Acc acc[TM][TN];
+    // ---------------------------------------------------------------- epilogue
+    // Lane (l & 31) owns output row m = m0 + 128 wm + 32 i + (l & 31); register 4 g + c of
+    // acc[i][j] is column n0 + 128 wn + 32 j + 8 g + 4 (l >> 5) + c.
+    //   y = round_out(fmaf((float)acc, a_scale[m] * w_scale[n], bias[n]))
+    auto epilogue = [&](int m0, int n0, int buf) {
+        const uint32_t *sc = scale_lds + buf * SCALE_WORDS;
+        constexpr int esz = OUT == OUT_F32 || OUT == OUT_I32 ? 4 : 2;
+        const int nl0 = wn * WAVE_N + 4 * (lane >> 5);
+        uint8_t *rowp[TM];
+        bool live[TM];
+        float as[TM];
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++) {
+            const int ml = wm * WAVE_M + 32 * i + frow;
+            live[i] = m0 + ml < M;
+            rowp[i] = (uint8_t *)ep.y + ((int64_t)min(m0 + ml, M - 1) * ep.ldy + n0 + nl0) * esz;
+            as[i] = SCALED ? __uint_as_float(sc[ml]) : 0.0f;
+        }
+        // the scale / bias operands of the lane's 4 columns at offset nc from its first column
+        auto operands = [&](int nc, float (&ws)[4], float (&bs)[4]) {
+            const v4i wv = *(const v4i *)(sc + BM + nl0 + nc);
 #pragma unroll
-        for (int j = 0; j < TN; j++)
+            for (int c = 0; c < 4; c++) ws[c] = __int_as_float(wv[c]);
+            const v4i bv = *(const v4i *)(sc + BM + BN + nl0 + nc);
+            if (!ep.bias) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
+                for (int c = 0; c < 4; c++) bs[c] = 0.0f;
+            } else if (ep.bias_dtype == PSQ_BF16) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) bs[c] = __uint_as_float((uint32_t)bv[c] << 16);
+            } else if (ep.bias_dtype == PSQ_F16) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) bs[c] = f16_to_f32((uint32_t)bv[c]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; c++) bs[c] = __int_as_float(bv[c]);
+            }
+        };
+        auto raw = [&](int i, int j, int r) { return agpr_read(acc[i][j][r]); };
+        auto value = [&](int i, int j, int r, float w, float b) {
+            const int x = raw(i, j, r);
+            const float a = FP8 ? __int_as_float(x) : (float)x;
+            return __builtin_fmaf(a, as[i] * w, b);
+        };
+        if (ep.vec && n0 + BN <= N) {
+            // full-width tile, aligned rows: one vector store per 4 columns
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int nc = 32 * j + 8 * g;
+                    float ws[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if constexpr (SCALED) operands(nc, ws, bs);
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        void *p = rowp[i] + nc * esz;
+                        const int r = 4 * g;
+                        if constexpr (OUT == OUT_I32) {
+                            const v4i o{raw(i, j, r), raw(i, j, r + 1), raw(i, j, r + 2), raw(i, j, r + 3)};
+                            if (live[i]) *(v4i *)p = o;
+                        } else if constexpr (OUT == OUT_F32) {
+                            const v4f o{value(i, j, r, ws[0], bs[0]), value(i, j, r + 1, ws[1], bs[1]),
+                                        value(i, j, r + 2, ws[2], bs[2]), value(i, j, r + 3, ws[3], bs[3])};
+                            if (live[i]) *(v4f *)p = o;
+                        } else {
+                            const v2i o{(int)pack2<OUT>(value(i, j, r, ws[0], bs[0]), value(i, j, r + 1, ws[1], bs[1])),
+                                        (int)pack2<OUT>(value(i, j, r + 2, ws[2], bs[2]),
+                                                        value(i, j, r + 3, ws[3], bs[3]))};
+                            if (live[i]) *(v2i *)p = o;
+                        }
+                    }
+                    // one column group at a time: keeps the scheduler from hoisting every group's
+                    // operand reads (and their registers) to the top of the epilogue
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        } else {
+            // partial tile or unaligned rows: element stores bounded by the row's remaining columns
+            const int n_left0 = N - (n0 + nl0);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int nc = 32 * j + 8 * g;
+                    float ws[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if constexpr (SCALED) operands(nc, ws, bs);
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        void *p = rowp[i] + nc * esz;
+#pragma unroll
+                        for (int c = 0; c < 4; c++) {
+                            if (!live[i] || c >= n_left0 - nc) continue;
+                            if constexpr (OUT == OUT_I32) ((int32_t *)p)[c] = raw(i, j, 4 * g + c);
+                            else store1<OUT>(p, c, value(i, j, 4 * g + c, ws[c], bs[c]));
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        }
+    };
 
-    const int nk = K / BK;
-    // Prologue: stages 0 .. NSTAGE-2 in flight.  Every step below issues exactly one stage (clamped
-    // to the last one, re-loading it into a ring slot nobody reads again), so the number of loads
-    // younger than the stage being waited for is always (NSTAGE - 2) LPS: the waits carry no branches.
+    // ---------------------------------------------------------------- main loop
+    point_at(v, 0, cu);
 #pragma unroll
-    for (int s = 0; s < NSTAGE - 1; s++) issue_stage(min(s, nk - 1), s);
+    for (int s = 0; s < NSTAGE - 1; s++) issue_stage(s, true, (int64_t)min(s, nk - 1) * BK);
     wait_vmcnt<(NSTAGE - 2) * LPS>();
     stage_barrier();
 
-    // One MFMA k-step g = KS * kt + ks: at the first k-step of stage kt refill the ring slot last
-    // read in stage kt - 1 (every wave passed the barrier that ended it); prefetch the fragments of
-    // step g + 1 into `nxt` -- after the stage's barrier when g + 1 opens a new stage -- then run
-    // the MFMAs of step g on `cur`.  Steps alternate between two register buffers in pairs, so the
-    // buffer roles are static.
-    auto kstep = [&](int g, FT (&ca)[TM], FT (&cw)[TN], FT (&na)[TM], FT (&nw)[TN]) {
-        const int kt = g / KS, ks = g - kt * KS;
-        if (ks == 0) issue_stage(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
-        if (ks + 1 < KS) {
-            read_frags(kt, ks + 1, na, nw);
-        } else {
-            wait_vmcnt<(NSTAGE - 2) * LPS>();   // stage kt + 1 landed for this wave ...
-            stage_barrier();         // ... and for every wave
-            read_frags(min(kt + 1, nk - 1), 0, na, nw);
-        }
-        mfma(acc, ca, cw);
-        if (ks == 0) interleave_with_mfma<LPS, TM + TN, TM * TN>();
-        else interleave_with_mfma<0, TM + TN, TM * TN>();
-    };
     FT fa0[TM], fw0[TN], fa1[TM], fw1[TN];
-    if constexpr (FP8) {
-        // fp8 fragments are 32 bytes: one register set (the allocator cannot double-buffer them
-        // beside 256 accumulators); a stage's reads still overlap its MFMAs in issue order.
-#pragma clang loop unroll(disable)
-        for (int kt = 0; kt < nk; kt++) {
-            issue_stage(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
-            read_frags(kt, 0, fa0, fw0);
-            mfma(acc, fa0, fw0);
-            // reads first (the MFMAs consume them in issue order), then one refill load per MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+    int rs = 0;                      // ring slot of the stage being computed
+    int buf = 0;                     // epilogue-operand buffer of the tile being computed
+    read_frags(0, 0, fa0, fw0);
+    // Stage kt loads stage kt + NSTAGE - 1: of this tile while that exists, else of the next
+    // tile (a K shorter than the lookahead gets one tile per workgroup, so it never gets there).
+    bool has_next = false;
+    auto issue_for = [&](int kt) {
+        const int t = kt + NSTAGE - 1;
+        const bool same = t < nk;
+        const int kk = same ? t : (has_next ? t - nk : nk - 1);
+        issue_stage(rs == 0 ? NSTAGE - 1 : rs - 1, same || !has_next, (int64_t)kk * BK);
+    };
+    // int8, one stage = two k-steps.  k-step 0: refill the ring slot read in the previous stage
+    // (every wave passed the barrier that ended it), prefetch k-step 1's fragments, MFMAs on
+    // k-step 0's.  k-step 1: wait for the next stage, barrier, prefetch its k-step 0 fragments,
+    // MFMAs on k-step 1's.
+    // fp8, one k-step per stage: the stages alternate between the two fragment sets; the first half
+    // of the MFMAs runs while the refill is issued, the second half overlaps the wait for the next
+    // stage and the read of its fragments.
+    auto stage = [&](int kt, FT (&ca)[TM], FT (&cw)[TN], FT (&na)[TM], FT (&nw)[TN]) {
+        issue_for(kt);
+        if constexpr (!FP8) {
+            read_frags(rs, 1, na, nw);
+            mfma(std::false_type{}, 0, TM, ca, cw);
+            interleave_with_mfma<LPS, TM + TN, TM * TN>();
+            wait_vmcnt<(NSTAGE - 2) * LPS>();
+            stage_barrier();
+            rs = rs == NSTAGE - 1 ? 0 : rs + 1;
+            read_frags(rs, 0, ca, cw);
+            mfma(std::false_type{}, 0, TM, na, nw);
+            interleave_with_mfma<0, TM + TN, TM * TN>();
+        } else {
+            mfma(std::false_type{}, 0, TM / 2, ca, cw);
 #pragma unroll
             for (int i = 0; i < LPS; i++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - LPS, 0);
             wait_vmcnt<(NSTAGE - 2) * LPS>();
             stage_barrier();
+            rs = rs == NSTAGE - 1 ? 0 : rs + 1;
+            read_frags(rs, 0, na, nw);
+            mfma(std::false_type{}, TM / 2, TM, ca, cw);
+            interleave_with_mfma<0, TM + TN, TM * TN / 2>();
         }
-    } else {
-        read_frags(0, 0, fa0, fw0);
-        const int steps = nk * KS;
+    };
 #pragma clang loop unroll(disable)
-        for (int g = 0; g < steps; g += 2) {
-            kstep(g, fa0, fw0, fa1, fw1);
-            if (g + 1 < steps) kstep(g + 1, fa1, fw1, fa0, fw0);
-        }
-    }
-
-    // ---------------------------------------------------------------- epilogue
-    // Each wave stages its 128 x 128 accumulators through its own 32 KB of the (now idle) LDS
-    // ring, 64 rows at a time, in row-major order; a lane then owns 4 consecutive columns of a
-    // row: y = round_out(fmaf(acc, a_scale[m] * w_scale[n], bias[n])), stored as full row segments.
-    // MFMA layout of a 32 x 32 tile: lane holds column (lane & 31) and, for register r, row
-    // 8 (r / 4) + 4 (lane / 32) + (r % 4).
-    wait_vmcnt<0>();   // the last (redundant) ring loads must land before the ring is reused
-    __syncthreads();   // every wave is done reading the ring
-    float *stage = (float *)(smem + wave * (32 * 1024));
-    const int col4 = (lane & 31) * 4;                 // the lane's 4 columns within the wave tile
-    const int nb = n0 + wn * WAVE_N + col4;           // first global column of the lane
-    float ws[4], bs[4];
+    for (; v < vend; v += step) {
+        int m0, n0;
+        tile_coords(v, nbm, nbn, m0, n0);
+        has_next = v + step < vend;
+        if (has_next) point_at(v + step, buf == NSCALEBUF - 1 ? 0 : buf + 1, nx);
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        ws[c] = (OUT == OUT_I32) ? 1.0f : s_ws[wn * WAVE_N + col4 + c];
-        bs[c] = (OUT == OUT_I32) ? 0.0f : s_b[wn * WAVE_N + col4 + c];
-    }
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-#pragma unroll
-        for (int il = 0; il < 2; il++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = il * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    const Acc &a = acc[2 * h + il][j];
-                    float v;
-                    if constexpr (OUT == OUT_I32 || !FP8) v = __int_as_float((int)a[r]);
-                    else v = a[r];
-                    stage[row * 128 + j * 32 + (lane & 31)] = v;
-                }
-#pragma unroll 4
-        for (int st = 0; st < 32; st++) {
-            const int row = 2 * st + (lane >> 5);
-            const v4f raw = *(const v4f *)(stage + row * 128 + col4);
-            // whole-vector reinterpretation only: hipcc mis-lowers __builtin_bit_cast applied to a
-            // single ext_vector element (it reads element 0)
-            const v4i rawi = __builtin_bit_cast(v4i, raw);
-            const int m = m0 + wm * WAVE_M + h * 64 + row;
-            if (m >= M) continue;
-            if constexpr (OUT == OUT_I32) {
-                int32_t *C = (int32_t *)ep.y + (int64_t)m * ep.ldy + nb;
-                if (ep.vec && nb + 3 < N) {
-                    *(v4i *)C = rawi;
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; c++)
-                        if (nb + c < N) C[c] = rawi[c];
-                }
-            } else {
-                const float as = s_as[wm * WAVE_M + h * 64 + row];
-                float y[4];
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const float accv = FP8 ? raw[c] : (float)rawi[c];
-                    y[c] = __builtin_fmaf(accv, as * ws[c], bs[c]);
-                }
-                store4<OUT>(ep.y, (int64_t)m * ep.ldy + nb, y, ep.vec && nb + 3 < N, N - nb);
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        if constexpr (!FP8) {
+            // int8 keeps fragment set 0 current at every stage boundary
+#pragma clang loop unroll(disable)
+            for (int kt = 0; kt < nk; kt++) stage(kt, fa0, fw0, fa1, fw1);
+        } else {
+            // fp8 swaps the sets per stage: pairs of stages (nk is even: K % 128 == 0)
+#pragma clang loop unroll(disable)
+            for (int kt = 0; kt < nk; kt += 2) {
+                stage(kt, fa0, fw0, fa1, fw1);
+                stage(kt + 1, fa1, fw1, fa0, fw0);
             }
         }
+        epilogue(m0, n0, buf);
+        buf = buf == NSCALEBUF - 1 ? 0 : buf + 1;
+        if (has_next) cu = nx;
     }
+    // the re-issued loads past the last tile must land before the workgroup's LDS is released
+    wait_vmcnt<0>();
 }
 
-constexpr size_t kSmemBytes = kRingBytes + 3 * 256 * sizeof(float);   // ring (>= the 128 KB epilogue stage) + scales
+// CUs of each device (the persistent grid size), cached per device.
+int cu_count(int dev)
+{
+    static int cus[64] = {};
+    if (dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
 
 template <bool FP8, int OUT>
 int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N, int64_t K,
@@ -382,8 +530,12 @@ int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int
             return set_error(PSQ_E_DEVICE, "%s: cannot reserve %zu bytes of LDS", name, kSmemBytes);
         attr_set[dev] = true;
     }
-    const int64_t nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    kern<<<dim3((unsigned)nblk), dim3(NTHREADS), kSmemBytes, st>>>(a, lda, w, ldw, (int)M, (int)N, (int)K, ep);
+    // persistent grid of one workgroup per CU; a K shorter than the ring's lookahead gets one
+    // workgroup per tile (the kernel's loads then never cross into another tile)
+    const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const bool short_k = K / BK < ring_depth<FP8>() - 1;
+    const int64_t grid = (short_k || tiles < cu_count(dev)) ? tiles : cu_count(dev);
+    kern<<<dim3((unsigned)grid), dim3(NTHREADS), kSmemBytes, st>>>(a, lda, w, ldw, (int)M, (int)N, (int)K, ep);
     return check_launch(name);
 }
 

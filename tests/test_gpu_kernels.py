@@ -172,8 +172,61 @@ def test_gemm_i8_epilogue(gpu, M, N, K, out_dtype, with_bias):
     assert_close_rms(y, ref, "int8 epilogue")
 
 
+# Problems with more 256 x 256 tiles than the GPU has CUs: the persistent GEMM runs several tiles
+# per workgroup, its loads cross into the next tile, and the epilogue operands rotate through
+# their buffers.  K = 128 is shorter than the load lookahead (one tile per workgroup); K = 256 has
+# the lookahead start at the very first stage; the 4100 x 4000 tiles are partial on both edges.
+PERSISTENT_CASES = [(4100, 4000, 512), (4352, 4352, 256), (4200, 4100, 128), (8200, 2000, 384)]
+
+
+@pytest.mark.parametrize("M,N,K", PERSISTENT_CASES)
+def test_gemm_i8_i32_persistent_bitexact(gpu, M, N, K):
+    from powershard_amd import ops
+    print(f"gemm_i8_i32 persistent M={M} N={N} K={K}", flush=True)
+    g = seeded(M + 3 * N + K)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    c = ops.gemm_i8_i32(a.to(gpu), w.to(gpu))
+    assert_bitexact(c, oracle.gemm_i8_i32(a, w), "int32 acc")
+
+
+@pytest.mark.parametrize("M,N,K", PERSISTENT_CASES[:2])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_gemm_i8_epilogue_persistent(gpu, M, N, K, out_dtype):
+    from powershard_amd import ops
+    print(f"gemm_i8 persistent M={M} N={N} K={K} {out_dtype}", flush=True)
+    g = seeded(M + N)
+    qa = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    sa = torch.rand(M, generator=g) * 0.05 + 1e-3
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.rand(N, generator=g) * 1e-3 + 1e-5
+    b = (torch.randn(N, generator=g) * 0.5).to(out_dtype)
+    y = ops.gemm_i8(qa.to(gpu), sa.to(gpu), qw.to(gpu), sw.to(gpu), b.to(gpu), out_dtype=out_dtype)
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, qw), sa, sw, b, out_dtype=out_dtype)
+    assert_bitexact(y, ref, "int8 epilogue output")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gemm_i8_epilogue_subnormal(gpu, out_dtype):
+    """Scales whose product is an fp32 subnormal: the epilogue keeps subnormals (no flush to zero)
+    and rounds them to bf16 as the oracle does."""
+    from powershard_amd import ops
+    M, N, K = 300, 512, 256
+    g = seeded(77)
+    qa = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sa = torch.full((M,), 1e-38) * (1 + torch.rand(M, generator=g))
+    sw = torch.rand(N, generator=g) * 1e-6
+    y = ops.gemm_i8(qa.to(gpu), sa.to(gpu), qw.to(gpu), sw.to(gpu), None, out_dtype=out_dtype)
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, qw), sa, sw, None, out_dtype=out_dtype)
+    r = ref.float().abs()
+    assert ((r != 0) & (r < 2.0 ** -126)).float().mean() > 0.5   # mostly subnormal outputs, not zeros
+    assert_bitexact(y, ref, "subnormal epilogue output")
+
+
 # ---------------------------------------------------------------------------- fp8
-@pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1000, 520, 5120), (17, 33, 128), (129, 777, 1024)])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1000, 520, 5120), (17, 33, 128), (129, 777, 1024),
+                                   (4100, 4000, 512), (4352, 4352, 256)])
 @pytest.mark.parametrize("per_row", [False, True])
 def test_gemm_fp8(gpu, M, N, K, per_row):
     from powershard_amd import ops
