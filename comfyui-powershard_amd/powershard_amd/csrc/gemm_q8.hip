@@ -126,26 +126,6 @@ __device__ __forceinline__ void stage_barrier()
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Scheduling hints (masks: 0x008 MFMA, 0x020 VMEM read, 0x100 DS read).  With one wave per
-// SIMD every issue slot not spent on an MFMA idles the matrix core, so the global->LDS loads of a
-// refill and the LDS fragment reads of the next k-step are each slotted behind an MFMA: the loads
-// first (they follow only reads the first MFMA already waited for), then the reads.
-template <int N_VMEM, int N_DS, int N_MFMA>
-__device__ __forceinline__ void interleave_with_mfma()
-{
-    static_assert(N_VMEM + N_DS <= N_MFMA, "one memory instruction per MFMA at most");
-#pragma unroll
-    for (int i = 0; i < N_VMEM; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < N_DS; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, (N_MFMA - N_VMEM) / N_DS, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-}
-
 template <bool FP8> struct Frag;
 template <> struct Frag<false> { typedef v4i T; static constexpr int KSTEP = 32; };   // 32x32x32 i8
 template <> struct Frag<true> { typedef v8i T; static constexpr int KSTEP = 64; };    // 32x32x64 f8f6f4
@@ -243,7 +223,8 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     // its last tile a workgroup re-issues the tile's last stage, a load into a ring slot nobody
     // reads again, so every stage issues the same number of loads and the waits are static.
     struct Ptrs { const uint8_t *a[LOADS], *w[LOADS]; };
-    Ptrs cu, nx;
+    Ptrs cu;                                  // the current tile's rows
+    int64_t da[LOADS] = {}, dw[LOADS] = {};   // next tile's rows minus the current tile's
     auto point_at = [&](int tv, int buf, Ptrs &p) {
         int m0, n0;
         tile_coords(tv, nbm, nbn, m0, n0);
@@ -268,54 +249,56 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             }
         }
     };
-    // load stage `koff` of the current tile (same) or of the next one into ring slot `slot`
+    // ring load q of a stage (q < LOADS: A block q, else W block q - LOADS), from the current tile
+    // (same) or the next one, at byte offset koff along K, into ring slot `slot`
+    // (the next tile's address is formed by adding a masked delta, not by selecting between two
+    // pointer sets: a select of pointers gets turned into a load from a selected address, which
+    // sends both sets to scratch memory)
+    auto issue_one = [&](int slot, bool same, int64_t koff, int q) {
+        const int j = q % LOADS, b = j * (NTHREADS / 64) + wave;
+        lds_ptr d = (lds_ptr)(smem + slot * 2 * STAGE_BYTES + (q < LOADS ? 0 : STAGE_BYTES) + 1024 * b);
+        const int64_t mask = same ? 0 : -1;
+        const uint8_t *g = q < LOADS ? cu.a[j] + (da[j] & mask) : cu.w[j] + (dw[j] & mask);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(g + koff), d, 16, 0, 0);
+    };
     auto issue_stage = [&](int slot, bool same, int64_t koff) {
-        lds_ptr dA = (lds_ptr)(smem + slot * 2 * STAGE_BYTES);
 #pragma unroll
-        for (int j = 0; j < LOADS; j++) {
-            const int b = j * (NTHREADS / 64) + wave;
-            const uint8_t *ga = (same ? cu.a[j] : nx.a[j]) + koff;
-            const uint8_t *gw = (same ? cu.w[j] : nx.w[j]) + koff;
-            __builtin_amdgcn_global_load_lds((glb_ptr)ga, dA + 1024 * b, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((glb_ptr)gw, dA + STAGE_BYTES + 1024 * b, 16, 0, 0);
-        }
+        for (int q = 0; q < LPS; q++) issue_one(slot, same, koff, q);
     };
 
     // MFMA operand layout (32 x 32 tiles): lane holds row (lane & 31) of W / of A and the k-slice
     // (lane >> 5) of the instruction's K; both operands use the same slice, so the dot products are
     // complete whatever order the hardware sums a slice in.
     const int frow = lane & 31, fk = lane >> 5;
-    auto read_frags = [&](int slot, int ks, FT (&fa)[TM], FT (&fw)[TN]) {
-        const uint8_t *sA = smem + slot * 2 * STAGE_BYTES;
-        const uint8_t *sW = sA + STAGE_BYTES;
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const int r = wm * WAVE_M + i * 32 + frow;
-            if constexpr (FP8) fa[i] = *(const v8i *)(sA + swz<true>(r, 2 * fk));
-            else fa[i] = *(const v4i *)(sA + swz<false>(r, 2 * ks + fk));
-        }
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int r = wn * WAVE_N + j * 32 + frow;
-            if constexpr (FP8) fw[j] = *(const v8i *)(sW + swz<true>(r, 2 * fk));
-            else fw[j] = *(const v4i *)(sW + swz<false>(r, 2 * ks + fk));
+    // fragment q of a k-step: q < TM is A fragment q, else W fragment q - TM
+    auto read_frag = [&](int slot, int ks, int q, FT (&fa)[TM], FT (&fw)[TN]) {
+        const uint8_t *base = smem + slot * 2 * STAGE_BYTES + (q < TM ? 0 : STAGE_BYTES);
+        const int r = (q < TM ? wm * WAVE_M + q * 32 : wn * WAVE_N + (q - TM) * 32) + frow;
+        if constexpr (FP8) {
+            // two 16-byte reads: the compiler otherwise makes every 32-byte read wait for all
+            // global->LDS loads in flight (vmcnt(0)), whose completion the stage wait and barrier
+            // already order
+            const v4i lo = *(const v4i *)(base + swz<true>(r, 2 * fk));
+            const v4i hi = *(const v4i *)(base + swz<true>(r, 2 * fk) + 16);
+            const v8i f = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if (q < TM) fa[q] = f;
+            else fw[q - TM] = f;
+        } else {
+            const v4i f = *(const v4i *)(base + swz<false>(r, 2 * ks + fk));
+            if (q < TM) fa[q] = f;
+            else fw[q - TM] = f;
         }
     };
     // acc[i][j] is the transposed 32 x 32 tile: W rows (output columns) x A rows (output rows).
-    // ZERO starts a tile: the accumulator input is the constant 0.
     Acc acc[TM][TN];
-    auto mfma = [&](auto zero, int i0, int i1, const FT (&fa)[TM], const FT (&fw)[TN]) {
-#pragma unroll
-        for (int i = i0; i < i1; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const Acc c = decltype(zero)::value ? Acc{} : acc[i][j];
-                if constexpr (FP8)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], c, 0, 0, 0, 127, 0, 127);
-                else
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], c, 0, 0, 0);
-            }
+    auto mfma = [&](int i, int j, const FT (&fa)[TM], const FT (&fw)[TN]) {
+        if constexpr (FP8)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+        else
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
     };
+    // Reads in the order the MFMAs (row-major over i, j) first need them: A0, W0..W3, A1..A3.
+    constexpr int kReadOrder[TM + TN] = {0, 4, 5, 6, 7, 1, 2, 3};
 
     // ---------------------------------------------------------------- epilogue
     // Lane (l & 31) owns output row m = m0 + 128 wm + 32 i + (l & 31); register 4 g + c of
@@ -362,33 +345,61 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             return __builtin_fmaf(a, as[i] * w, b);
         };
         if (ep.vec && n0 + BN <= N) {
-            // full-width tile, aligned rows: one vector store per 4 columns
+            // Full-width tile, aligned rows.  Lanes l and l + 32 hold the same row: for column
+            // groups g = 2p and 2p + 1 lane l has columns 16p + {0-3, 8-11} and lane l + 32 has
+            // 16p + {4-7, 12-15}.  One v_permlane32_swap per word gives lane l columns 16p + 0-7
+            // and lane l + 32 columns 16p + 8-15, so each store writes 8 consecutive outputs and a
+            // row's 16 columns take one instruction (half the stores, twice the bytes per line).
 #pragma unroll
             for (int j = 0; j < TN; j++)
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const int nc = 32 * j + 8 * g;
-                    float ws[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if constexpr (SCALED) operands(nc, ws, bs);
+                for (int pr = 0; pr < 2; pr++) {
+                    const int nc = 32 * j + 16 * pr;
+                    float ws[2][4] = {{1.0f, 1.0f, 1.0f, 1.0f}, {1.0f, 1.0f, 1.0f, 1.0f}};
+                    float bs[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+                    if constexpr (SCALED) {
+                        operands(nc, ws[0], bs[0]);
+                        operands(nc + 8, ws[1], bs[1]);
+                    }
 #pragma unroll
                     for (int i = 0; i < TM; i++) {
-                        void *p = rowp[i] + nc * esz;
-                        const int r = 4 * g;
-                        if constexpr (OUT == OUT_I32) {
-                            const v4i o{raw(i, j, r), raw(i, j, r + 1), raw(i, j, r + 2), raw(i, j, r + 3)};
-                            if (live[i]) *(v4i *)p = o;
-                        } else if constexpr (OUT == OUT_F32) {
-                            const v4f o{value(i, j, r, ws[0], bs[0]), value(i, j, r + 1, ws[1], bs[1]),
-                                        value(i, j, r + 2, ws[2], bs[2]), value(i, j, r + 3, ws[3], bs[3])};
-                            if (live[i]) *(v4f *)p = o;
-                        } else {
-                            const v2i o{(int)pack2<OUT>(value(i, j, r, ws[0], bs[0]), value(i, j, r + 1, ws[1], bs[1])),
-                                        (int)pack2<OUT>(value(i, j, r + 2, ws[2], bs[2]),
-                                                        value(i, j, r + 3, ws[3], bs[3]))};
-                            if (live[i]) *(v2i *)p = o;
+                        // words of the two groups: x (g = 2 pr), y (g = 2 pr + 1)
+                        constexpr int NW = esz == 4 ? 4 : 2;
+                        uint32_t x[NW], y[NW];
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            uint32_t *o = h == 0 ? x : y;
+                            const int r = 8 * pr + 4 * h;
+                            if constexpr (OUT == OUT_I32) {
+#pragma unroll
+                                for (int c = 0; c < 4; c++) o[c] = (uint32_t)raw(i, j, r + c);
+                            } else if constexpr (OUT == OUT_F32) {
+#pragma unroll
+                                for (int c = 0; c < 4; c++) o[c] = __float_as_uint(value(i, j, r + c, ws[h][c], bs[h][c]));
+                            } else {
+                                o[0] = pack2<OUT>(value(i, j, r, ws[h][0], bs[h][0]), value(i, j, r + 1, ws[h][1], bs[h][1]));
+                                o[1] = pack2<OUT>(value(i, j, r + 2, ws[h][2], bs[h][2]), value(i, j, r + 3, ws[h][3], bs[h][3]));
+                            }
+                        }
+                        uint32_t lo[NW], hi[NW];
+#pragma unroll
+                        for (int d = 0; d < NW; d++) {
+                            const auto sw = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
+                            lo[d] = sw[0];
+                            hi[d] = sw[1];
+                        }
+                        // lane l < 32 stores at column nc, lane l + 32 at nc + 8 (rowp already holds 4 h)
+                        uint8_t *p = rowp[i] + (nc + 4 * (lane >> 5)) * esz;
+                        if (live[i]) {
+                            if constexpr (NW == 2) {
+                                *(v4i *)p = v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                            } else {
+                                *(v4i *)p = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+                                *(v4i *)(p + 16) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+                            }
                         }
                     }
-                    // one column group at a time: keeps the scheduler from hoisting every group's
+                    // one column pair at a time: keeps the scheduler from hoisting every group's
                     // operand reads (and their registers) to the top of the epilogue
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -427,48 +438,60 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     FT fa0[TM], fw0[TN], fa1[TM], fw1[TN];
     int rs = 0;                      // ring slot of the stage being computed
     int buf = 0;                     // epilogue-operand buffer of the tile being computed
-    read_frags(0, 0, fa0, fw0);
+#pragma unroll
+    for (int q = 0; q < TM + TN; q++) read_frag(0, 0, q, fa0, fw0);
     // Stage kt loads stage kt + NSTAGE - 1: of this tile while that exists, else of the next
     // tile (a K shorter than the lookahead gets one tile per workgroup, so it never gets there).
     bool has_next = false;
-    auto issue_for = [&](int kt) {
-        const int t = kt + NSTAGE - 1;
-        const bool same = t < nk;
-        const int kk = same ? t : (has_next ? t - nk : nk - 1);
-        issue_stage(rs == 0 ? NSTAGE - 1 : rs - 1, same || !has_next, (int64_t)kk * BK);
-    };
-    // int8, one stage = two k-steps.  k-step 0: refill the ring slot read in the previous stage
-    // (every wave passed the barrier that ended it), prefetch k-step 1's fragments, MFMAs on
-    // k-step 0's.  k-step 1: wait for the next stage, barrier, prefetch its k-step 0 fragments,
-    // MFMAs on k-step 1's.
-    // fp8, one k-step per stage: the stages alternate between the two fragment sets; the first half
-    // of the MFMAs runs while the refill is issued, the second half overlaps the wait for the next
-    // stage and the read of its fragments.
+    // The instruction order inside a stage is fixed explicitly (sched_barrier after every step):
+    // with one wave per SIMD every issue slot not spent on an MFMA idles the matrix core, and the
+    // wave stalls wherever it waits for LDS reads still in flight.  So each half-stage first slots
+    // the fragment reads the next half-stage consumes behind its first MFMAs (they then have the
+    // rest of the half-stage to land), then the refill loads behind the following ones.
+    //   int8, one stage = two k-steps.  Half A: MFMAs of k-step 0 on (ca, cw); behind them the
+    //   reads of k-step 1 into (na, nw) and the refill of the ring slot read in the previous stage
+    //   (every wave passed the barrier that ended it).  Wait for the next stage, barrier.  Half B:
+    //   MFMAs of k-step 1 on (na, nw); behind them the next stage's k-step 0 reads into (ca, cw).
+    //   fp8, one k-step per stage.  Half A: MFMAs of rows 0-1 on (ca, cw) with the refill loads;
+    //   wait, barrier; half B: MFMAs of rows 2-3 with the next stage's reads into (na, nw).
     auto stage = [&](int kt, FT (&ca)[TM], FT (&cw)[TN], FT (&na)[TM], FT (&nw)[TN]) {
-        issue_for(kt);
+        const int t = kt + NSTAGE - 1;
+        const bool same = t < nk || !has_next;
+        const int64_t koff = (int64_t)(t < nk ? t : (has_next ? t - nk : nk - 1)) * BK;
+        const int slot = rs == 0 ? NSTAGE - 1 : rs - 1;
         if constexpr (!FP8) {
-            read_frags(rs, 1, na, nw);
-            mfma(std::false_type{}, 0, TM, ca, cw);
-            interleave_with_mfma<LPS, TM + TN, TM * TN>();
-            wait_vmcnt<(NSTAGE - 2) * LPS>();
-            stage_barrier();
-            rs = rs == NSTAGE - 1 ? 0 : rs + 1;
-            read_frags(rs, 0, ca, cw);
-            mfma(std::false_type{}, 0, TM, na, nw);
-            interleave_with_mfma<0, TM + TN, TM * TN>();
-        } else {
-            mfma(std::false_type{}, 0, TM / 2, ca, cw);
 #pragma unroll
-            for (int i = 0; i < LPS; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            for (int q = 0; q < TM * TN; q++) {
+                mfma(q / TN, q % TN, ca, cw);
+                if (q < TM + TN) read_frag(rs, 1, kReadOrder[q], na, nw);
+                else issue_one(slot, same, koff, q - (TM + TN));
+                __builtin_amdgcn_sched_barrier(0);
             }
             wait_vmcnt<(NSTAGE - 2) * LPS>();
             stage_barrier();
             rs = rs == NSTAGE - 1 ? 0 : rs + 1;
-            read_frags(rs, 0, na, nw);
-            mfma(std::false_type{}, TM / 2, TM, ca, cw);
-            interleave_with_mfma<0, TM + TN, TM * TN / 2>();
+#pragma unroll
+            for (int q = 0; q < TM * TN; q++) {
+                mfma(q / TN, q % TN, na, nw);
+                if (q < TM + TN) read_frag(rs, 0, kReadOrder[q], ca, cw);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < TM * TN / 2; q++) {
+                mfma(q / TN, q % TN, ca, cw);
+                issue_one(slot, same, koff, q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            wait_vmcnt<(NSTAGE - 2) * LPS>();
+            stage_barrier();
+            rs = rs == NSTAGE - 1 ? 0 : rs + 1;
+#pragma unroll
+            for (int q = 0; q < TM * TN / 2; q++) {
+                mfma(TM / 2 + q / TN, q % TN, ca, cw);
+                read_frag(rs, 0, kReadOrder[q], na, nw);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
 #pragma clang loop unroll(disable)
@@ -476,7 +499,15 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         int m0, n0;
         tile_coords(v, nbm, nbn, m0, n0);
         has_next = v + step < vend;
-        if (has_next) point_at(v + step, buf == NSCALEBUF - 1 ? 0 : buf + 1, nx);
+        if (has_next) {
+            Ptrs nx;
+            point_at(v + step, buf == NSCALEBUF - 1 ? 0 : buf + 1, nx);
+#pragma unroll
+            for (int j = 0; j < LOADS; j++) {
+                da[j] = nx.a[j] - cu.a[j];
+                dw[j] = nx.w[j] - cu.w[j];
+            }
+        }
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -497,7 +528,13 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         }
         epilogue(m0, n0, buf);
         buf = buf == NSCALEBUF - 1 ? 0 : buf + 1;
-        if (has_next) cu = nx;
+        if (has_next) {
+#pragma unroll
+            for (int j = 0; j < LOADS; j++) {
+                cu.a[j] += da[j];
+                cu.w[j] += dw[j];
+            }
+        }
     }
     // the re-issued loads past the last tile must land before the workgroup's LDS is released
     wait_vmcnt<0>();
