@@ -24,6 +24,9 @@ namespace {
 #ifndef PSQ_Q8_SWZ
 #define PSQ_Q8_SWZ 1
 #endif
+#ifndef PSQ_Q8_SCHED
+#define PSQ_Q8_SCHED 1
+#endif
 #ifndef PSQ_Q8_GROUP_M
 #define PSQ_Q8_GROUP_M 8
 #endif
@@ -299,6 +302,31 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     };
     // Reads in the order the MFMAs (row-major over i, j) first need them: A0, W0..W3, A1..A3.
     constexpr int kReadOrder[TM + TN] = {0, 4, 5, 6, 7, 1, 2, 3};
+    // int8 half-stage schedules: behind MFMA q, fragment read kSchedRead[q] and ring load
+    // kSchedLoadA[q] (first half) / kSchedLoadB[q] (second half); -1 = none.  Global->LDS loads
+    // issued back to back stall the wave's MFMA issue, so they are spaced out; the reads go first.
+#if PSQ_Q8_SCHED == 0
+    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
+    constexpr int kSchedLoadA[16] = {-1, -1, -1, -1, -1, -1, -1, -1, 0, 1, 2, 3, 4, 5, 6, 7};
+    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
+#elif PSQ_Q8_SCHED == 1
+    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
+    constexpr int kSchedLoadA[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, 0, -1, 1, -1, 2, -1, 3};
+    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, 4, -1, 5, -1, 6, -1, 7};
+#elif PSQ_Q8_SCHED == 2
+    constexpr int kSchedRead[16] = {0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7, -1};
+    constexpr int kSchedLoadA[16] = {-1, 0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7};
+    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
+#else
+    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
+    constexpr int kSchedLoadA[16] = {-1, -1, -1, 0, -1, -1, -1, 1, -1, -1, -1, 2, -1, -1, -1, 3};
+    constexpr int kSchedLoadB[16] = {-1, -1, -1, 4, -1, -1, -1, 5, -1, -1, -1, 6, -1, -1, -1, 7};
+#endif
+    constexpr int kLoadsB = [] {
+        int n = 0;
+        for (int q = 0; q < 16; q++) n += kSchedLoadB[q] >= 0;
+        return n;
+    }();
 
     // ---------------------------------------------------------------- epilogue
     // Lane (l & 31) owns output row m = m0 + 128 wm + 32 i + (l & 31); register 4 g + c of
@@ -463,17 +491,18 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
 #pragma unroll
             for (int q = 0; q < TM * TN; q++) {
                 mfma(q / TN, q % TN, ca, cw);
-                if (q < TM + TN) read_frag(rs, 1, kReadOrder[q], na, nw);
-                else issue_one(slot, same, koff, q - (TM + TN));
+                if (kSchedRead[q] >= 0) read_frag(rs, 1, kReadOrder[kSchedRead[q]], na, nw);
+                if (kSchedLoadA[q] >= 0) issue_one(slot, same, koff, kSchedLoadA[q]);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            wait_vmcnt<(NSTAGE - 2) * LPS>();
+            wait_vmcnt<(NSTAGE - 2) * LPS - kLoadsB>();
             stage_barrier();
             rs = rs == NSTAGE - 1 ? 0 : rs + 1;
 #pragma unroll
             for (int q = 0; q < TM * TN; q++) {
                 mfma(q / TN, q % TN, na, nw);
-                if (q < TM + TN) read_frag(rs, 0, kReadOrder[q], ca, cw);
+                if (kSchedRead[q] >= 0) read_frag(rs, 0, kReadOrder[kSchedRead[q]], ca, cw);
+                if (kSchedLoadB[q] >= 0) issue_one(slot, same, koff, kSchedLoadB[q]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
