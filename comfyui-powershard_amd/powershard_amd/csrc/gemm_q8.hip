@@ -55,23 +55,11 @@ struct Epi {
     int vec;          // rows of y are 16-byte aligned: 4-element vector stores allowed
 };
 
-// Four consecutive outputs packed for one vector store: 2 words of bf16 / f16 (round to nearest
-// even), or 4 words of fp32 / int32 bits.
-#ifndef PSQ_NATIVE_BF16
-#define PSQ_NATIVE_BF16 1
-#endif
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
+// Two outputs packed for a vector store (round to nearest even).
 template <int OUT>
 __device__ __forceinline__ uint32_t pack2(float a, float b)
 {
-    if constexpr (OUT == OUT_BF16 && PSQ_NATIVE_BF16) {
-        // v_cvt_pk_bf16_f32: round to nearest even, as f32_to_bf16 (NaN inputs give a quiet NaN)
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-    } else {
-        return f32_to_half<OUT>(a) | (f32_to_half<OUT>(b) << 16);
-    }
+    return pack_half2<OUT == OUT_BF16 ? PSQ_BF16 : PSQ_F16>(a, b);
 }
 
 // One output element (the slow path of partial tiles and unaligned outputs).

@@ -55,7 +55,7 @@ __device__ __forceinline__ int xswz(int row, int chunk) { return row * XROW + ((
 template <int XDT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi)
 {
-    return f32_to_half<XDT>(lo) | (f32_to_half<XDT>(hi) << 16);
+    return pack_half2<XDT>(lo, hi);
 }
 
 template <int XDT, int WK>
@@ -220,10 +220,148 @@ gemm_wonly_kernel(const uint16_t *__restrict__ X, int64_t ldx, int M, int N, int
     }
 }
 
+// Skinny weight-only GEMM (M <= 64, the decode / text-encoder shapes, bound by the weight stream):
+// one workgroup per 16 weight rows (output columns) whose 4 waves split K by 128-element blocks
+// round-robin.  Per block a lane streams the 32 consecutive k of one weight row that belong to its
+// lane group (16 bytes of nibbles / 32 bytes of int8), dequantizes them in registers for four
+// 16x16x32 MFMA k-steps, and reads the matching 16-byte activation fragments straight from memory
+// (the activations are small and stay in L2).  The MFMA sums over a k set per lane group; both
+// operands use the same assignment, so every dot product is complete.  The four waves' partial
+// tiles are added through LDS in a fixed order, then the epilogue of the tiled kernel applies.
+constexpr int SK_BLOCK = 128;                  // k per block: 4 lane groups x 32
+
+template <int XDT, int WK, int MT>
+__global__ void __launch_bounds__(NTHREADS)
+gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
+{
+    __shared__ float red[4][MT][16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int nr = lane & 15, h = lane >> 4;
+    const int n = min(n0 + nr, N - 1);
+    constexpr int WROW_DIV = WK == W_UINT4 ? 2 : 1;
+    const uint8_t *wrow = wa.wq + (int64_t)n * (K / WROW_DIV);
+    const uint16_t *xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) xrow[mt] = x + (int64_t)min(16 * mt + nr, M - 1) * ldx;
+    const int G = WK == W_UINT4 ? K / wa.gs : 1;
+    using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
+
+    v4f acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    constexpr int NW = WK == W_UINT4 ? 4 : 8;       // weight words per lane per block
+    const int nblk = K / SK_BLOCK;
+    // The weight stream is software-pipelined one block deep (the next block's words and group
+    // scale / zero load while this block computes); the activation fragments, L2 hits, load at the
+    // top of each block.
+    struct WBlock { uint32_t w[NW]; float s, z; };
+    auto load_w = [&](int b, WBlock &r) {
+        const int kb = b * SK_BLOCK + 32 * h;
+        const v4i t0 = *(const v4i *)(wrow + kb / WROW_DIV);
+#pragma unroll
+        for (int c = 0; c < 4; c++) r.w[c] = (uint32_t)t0[c];
+        if constexpr (WK == W_INT8) {
+            const v4i t1 = *(const v4i *)(wrow + kb + 16);
+#pragma unroll
+            for (int c = 0; c < 4; c++) r.w[4 + c] = (uint32_t)t1[c];
+            r.s = 1.0f;
+            r.z = 0.0f;
+        } else {
+            const int64_t gi = (int64_t)n * G + kb / wa.gs;
+            r.s = f16_to_f32(wa.scale16[gi]);
+            r.z = f16_to_f32(wa.zero16[gi]);
+        }
+    };
+    auto compute = [&](int b, const WBlock &r) {
+        const int kb = b * SK_BLOCK + 32 * h;        // the lane group's first k
+        v4i xv[4][MT];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) xv[t][mt] = *(const v4i *)(xrow[mt] + kb + 8 * t);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            // weights of k = kb + 8t .. kb + 8t + 7
+            uint32_t hw[4];
+            if constexpr (WK == W_UINT4) {
+                const uint32_t p = r.w[t];
+                const uint32_t lo = p & 0x0f0f0f0fu, hi = (p >> 4) & 0x0f0f0f0fu;   // even / odd k
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float q0 = (float)((lo >> (8 * e)) & 0xffu);
+                    const float q1 = (float)((hi >> (8 * e)) & 0xffu);
+                    hw[e] = pack2<XDT>((q0 - r.z) * r.s, (q1 - r.z) * r.s);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t p = r.w[2 * t + e];
+                    hw[2 * e] = pack2<XDT>((float)(int8_t)(p & 0xffu), (float)(int8_t)((p >> 8) & 0xffu));
+                    hw[2 * e + 1] = pack2<XDT>((float)(int8_t)((p >> 16) & 0xffu), (float)(int8_t)(p >> 24));
+                }
+            }
+            const XV wf = __builtin_bit_cast(XV, v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]});
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const XV xf = __builtin_bit_cast(XV, xv[t][mt]);
+                if constexpr (XDT == PSQ_BF16)
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xf, acc[mt], 0, 0, 0);
+                else
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, xf, acc[mt], 0, 0, 0);
+            }
+        }
+    };
+    WBlock cur, nxt;
+    if (wave < nblk) load_w(wave, cur);
+    for (int b = wave; b < nblk; b += 4) {
+        if (b + 4 < nblk) load_w(b + 4, nxt);
+        compute(b, cur);
+        cur = nxt;
+    }
+    // acc[mt] is the 16 x 16 tile C[n][m]: lane holds m = 16 mt + (lane & 15), n = 4 (lane >> 4) + v
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) red[wave][mt][4 * h + v][nr] = acc[mt][v];
+    __syncthreads();
+#pragma unroll
+    for (int o = tid; o < MT * 256; o += NTHREADS) {
+        const int mt = o >> 8, ml = (o >> 4) & 15, nl = o & 15;
+        const int m = 16 * mt + ml, nn = n0 + nl;
+        if (m >= M || nn >= N) continue;
+        const float sum = ((red[0][mt][nl][ml] + red[1][mt][nl][ml]) + red[2][mt][nl][ml]) + red[3][mt][nl][ml];
+        const float cs = (WK == W_INT8) ? wa.scale32[nn] : 1.0f;
+        const float bb = wa.bias ? load_elem(wa.bias, nn, wa.bias_dtype) : 0.0f;
+        store_elem(wa.y, (int64_t)m * wa.ldy + nn, wa.y_dtype, __builtin_fmaf(sum, cs, bb));
+    }
+}
+
+template <int XDT, int WK>
+void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st)
+{
+    const dim3 grid((unsigned)((N + 15) / 16)), block(NTHREADS);
+    const int mt = (int)((M + 15) / 16);
+    if (mt == 1) gemm_wonly_skinny<XDT, WK, 1><<<grid, block, 0, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    else if (mt == 2) gemm_wonly_skinny<XDT, WK, 2><<<grid, block, 0, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    else if (mt == 3) gemm_wonly_skinny<XDT, WK, 3><<<grid, block, 0, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    else gemm_wonly_skinny<XDT, WK, 4><<<grid, block, 0, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+}
+
+// The skinny kernel takes M <= SKINNY_MAX_M when K is a whole number of 128-element blocks (and,
+// for uint4, the groups hold whole 32-element lane runs); the tiled kernel takes the rest.
+constexpr int64_t SKINNY_MAX_M = 64;
+
 template <int WK>
 int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa,
            hipStream_t st, const char *name)
 {
+    if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (WK != W_UINT4 || wa.gs % 32 == 0)) {
+        if (x_dtype == PSQ_BF16) launch_skinny<PSQ_BF16, WK>((const uint16_t *)x, ldx, M, N, K, wa, st);
+        else launch_skinny<PSQ_F16, WK>((const uint16_t *)x, ldx, M, N, K, wa, st);
+        return check_launch(name);
+    }
     const int64_t nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     const dim3 grid((unsigned)nblk), block(NTHREADS);
     if (x_dtype == PSQ_BF16)

@@ -80,6 +80,21 @@ __device__ __forceinline__ uint32_t f32_to_half(float f)
     else return f32_to_f16(f);
 }
 
+// Two fp32 values rounded (nearest even) to a packed pair of DT (bf16 or f16), low half first:
+// one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32.  Finite results equal f32_to_half's, subnormals
+// included; a NaN input gives a quiet NaN.  opaque() keeps the backend from folding a producing
+// fma / mul into a mixed-precision instruction.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <int DT>
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi)
+{
+    const f32x2_t v{opaque(lo), opaque(hi)};
+    if constexpr (DT == PSQ_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+}
+
 // OCP e4m3fn decode.
 __device__ __forceinline__ float e4m3_to_f32(uint32_t c)
 {

@@ -247,8 +247,10 @@ def test_gemm_fp8(gpu, M, N, K, per_row):
 
 
 # ------------------------------------------------------------------- weight-only
+# M <= 64 with K % 128 == 0 runs the skinny (weight-streaming) kernel, the rest the tiled one
 @pytest.mark.parametrize("M,N,K,gs", [(512, 384, 1024, 128), (7, 256, 512, 64), (130, 100, 5120, 128),
-                                      (64, 1000, 256, 256)])
+                                      (64, 1000, 256, 256), (1, 2600, 5120, 128), (16, 513, 1024, 128),
+                                      (33, 64, 2048, 64), (65, 300, 1024, 128), (3, 100, 384, 64)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
     from powershard_amd import ops
@@ -264,7 +266,8 @@ def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
     assert_fp32_path(y32, yb, ref32, "w4a16 gemm")
 
 
-@pytest.mark.parametrize("M,N,K", [(1024, 512, 1024), (5, 40, 256), (200, 300, 5120)])
+@pytest.mark.parametrize("M,N,K", [(1024, 512, 1024), (5, 40, 256), (200, 300, 5120), (1, 1030, 5120),
+                                   (48, 256, 1024), (64, 64, 640)])
 def test_gemm_w8a16(gpu, M, N, K):
     from powershard_amd import ops
     x = heavy_rows(M, K, seed=M, outlier_frac=0)
