@@ -160,24 +160,47 @@ def headline(args):
     log(f"[bench] headline: {ms_clean:.3f} ms/step, {tops:.1f} TOPS; gemm {gemm_ms:.3f} ms = {gemm_tops:.1f} TOPS "
         f"({100 * gemm_tops / PEAK_INT8_TOPS:.1f}% of int8 peak); quant {quant_ms * 1e3:.1f} us = "
         f"{res['quant_gbs']:.0f} GB/s")
-    sample = dict(x=x[:512].cpu(), qdata=qt._qdata.cpu(), scale=qt._params.scale.cpu(), bias=b.cpu(), y=y[:512].cpu())
+    # parity rows: the first 64, 128 spread over the middle, and the last 64 (the partial last tile)
+    g = torch.Generator().manual_seed(5000 + cfg)
+    mid = torch.randperm(M - 128, generator=g)[:128] + 64
+    idx = torch.cat([torch.arange(64), mid.sort().values, torch.arange(M - 64, M)])
+    sample = dict(x=x[:8192].cpu(), qdata=qt._qdata.cpu(), scale=qt._params.scale.cpu(), bias=b.cpu(),
+                  rows=idx, x_rows=x[idx.to(x.device)].cpu(), y_rows=y[idx.to(y.device)].cpu())
     del layer, qt, x, y
     torch.cuda.empty_cache()
     return res, sample
 
 
 def check_headline_parity(sample):
-    """Bit-exact check of the headline's first rows against the oracle (quant + int32 + epilogue)."""
+    """Bit-exact check of 256 sampled rows of the headline output (first, spread, last -- the last
+    ones in the partial tile) against the oracle (rotate + quantize, int32 GEMM, epilogue)."""
     import torch
     import oracle
-    rows = 64
-    qa, sa = oracle.quantize_rows_i8(sample["x"][:rows], 256)
+    qa, sa = oracle.quantize_rows_i8(sample["x_rows"], 256)
     ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, sample["qdata"]), sa, sample["scale"], sample["bias"])
-    got = sample["y"][:rows]
+    got = sample["y_rows"]
     same = bool(torch.equal(got.view(torch.int16), ref.view(torch.int16)))
     err = (got.float() - ref.float()).abs().max().item()
     rms = ref.float().pow(2).mean().sqrt().item()
-    return dict(rows_checked=rows, bitexact=same, max_abs_err_over_rms=err / rms)
+    return dict(rows_checked=int(sample["rows"].numel()), bitexact=same, max_abs_err_over_rms=err / rms)
+
+
+PROFILE = os.path.join(ROOT, "profiles", "gemm_i8_w8a8_convrot_m32760_n13824_k5120.md")
+
+
+def profiled_traffic():
+    """HBM-side bytes per launch of the headline GEMM: FETCH_SIZE and WRITE_SIZE (rocprofv3 --pmc,
+    one counter per run) scaled by their copy-kernel calibration factors, as recorded in the
+    kernel's profile summary.  None when the summary is absent."""
+    try:
+        text = open(PROFILE).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        d = json.loads(block)
+        return dict(bytes=int(d["read_bytes"] + d["write_bytes"]),
+                    source=f"profiles/{os.path.basename(PROFILE)}: FETCH_SIZE x{d['fetch_factor']} "
+                           f"+ WRITE_SIZE x{d['write_factor']} per launch (L2 <-> fabric bytes)")
+    except (OSError, IndexError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(sample, target_s):
@@ -330,7 +353,7 @@ def main():
     _native.lib()
     h, sample = headline(args)
     parity = check_headline_parity(sample)
-    log(f"[bench] headline parity (64 rows vs oracle): {parity}")
+    log(f"[bench] headline parity ({parity['rows_checked']} sampled rows vs oracle): {parity}")
     cpu = None if args.no_cpu else cpu_baseline(sample, args.cpu_seconds)
     if cpu:
         log(f"[bench] cpu baseline: {cpu['value'] * 1e3:.1f} GOPS on {cpu['cores']} threads")
@@ -342,9 +365,11 @@ def main():
                 extra[name] = fn(args)
             except torch.cuda.OutOfMemoryError as e:
                 extra[name] = {"error": f"OOM: {e}"}
+    traffic = profiled_traffic()
     roof = dict(bound="mfma", achieved=h["gemm_tops"], peak=PEAK_INT8_TOPS, unit="TOPS",
-                frac=h["gemm_tops"] / PEAK_INT8_TOPS, traffic=None, kernel="gemm_i8",
-                kernel_ms=h["gemm_ms"], algorithmic_ops_per_launch=2.0 * h["M"] * h["N"] * h["K"])
+                frac=h["gemm_tops"] / PEAK_INT8_TOPS, traffic=traffic and traffic["bytes"], kernel="gemm_i8",
+                kernel_ms=h["gemm_ms"], algorithmic_ops_per_launch=2.0 * h["M"] * h["N"] * h["K"],
+                traffic_source=traffic and traffic["source"])
     line = {
         "metric": METRIC, "value": round(h["tops"], 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(h["ms_per_step"], 4), "higher_is_better": True,
