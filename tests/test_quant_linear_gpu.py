@@ -1,0 +1,135 @@
+"""QuantLinear end to end on the GPU: install, pack, forward through the native gfx950 kernels,
+checked against the CPU oracle (the module-level counterpart of test_quant_formats_torch.py:80-103
+in the reference, which compares QuantLinear with F.linear on the dequantized weight).
+
+* W8A8 (ConvRot and plain): bit-exact with the oracle for bf16 and f16 compute.
+* fp8 and int4: the fp32-accumulating bar of test_gpu_kernels (1e-2 rms or one output ulp).
+* The dequantize compute mode: equal to F.linear on the oracle-dequantized weight.
+* A shape the native kernels do not take warns once, switches the module to dequantize and still
+  returns the dequantize result (quant_linear.py:207-215 policy).
+"""
+import warnings
+
+import pytest
+import torch
+from torch import nn
+
+import oracle
+from conftest import heavy_rows, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def make_layer(K, N, weight_format, opts, compute_dtype, native, dev, seed, bias=True, follow_input=False):
+    from powershard_amd.quant_linear import install_quant_linears, quantized_from_float, pack
+    net = nn.Sequential(nn.Linear(K, N, bias=bias)).to(compute_dtype)
+    tensors = {"0.weight": {"key": "0.weight", "dtype": "BF16", "shape": [N, K]}}
+    install_quant_linears(net, tensors, weight_format, "native" if native else "dequantize", None, compute_dtype,
+                          dev, quant_options=opts, follow_input=follow_input)
+    layer = net[0]
+    g = seeded(seed)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    qt = quantized_from_float(w, layer._ps_qplan.fmt, **opts)
+    layer.qbytes = nn.Parameter(pack(qt, layer._ps_qplan, dev), requires_grad=False)
+    b = (torch.randn(N, generator=g) * 0.05).to(compute_dtype) if bias else None
+    layer.bias = None if b is None else nn.Parameter(b.to(dev), requires_grad=False)
+    return layer, qt, b
+
+
+def within_fp32_bar(y, ref):
+    y, ref = y.float().cpu(), ref.float().cpu()
+    rms = ref.pow(2).mean().sqrt().item()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(ref.abs().clamp(min=1e-30))) - 7)
+    bound = torch.maximum(torch.full_like(ref, 1e-2 * rms), ulp)
+    err = (y - ref).abs()
+    assert torch.all(err <= bound), f"max err {err.max().item():.3e} vs rms {rms:.3e}"
+
+
+@pytest.mark.parametrize("convrot", [True, False])
+@pytest.mark.parametrize("compute_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bias", [True, False])
+def test_w8a8_quantlinear_bitexact(gpu, convrot, compute_dtype, bias):
+    K, N = 1024, 768
+    opts = {"convrot": convrot, "convrot_groupsize": 256} if convrot else {"convrot": False}
+    layer, qt, b = make_layer(K, N, "int8", opts, compute_dtype, True, gpu, seed=11, bias=bias)
+    x = heavy_rows(2 * 77, K, seed=12, dtype=compute_dtype).reshape(2, 77, K)   # leading dims flatten
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")      # the native path must not fall back
+        y = layer(x.to(gpu))
+    assert layer._ps_native and y.shape == (2, 77, N) and y.dtype == compute_dtype
+    qa, sa = oracle.quantize_rows_i8(x.reshape(-1, K), 256 if convrot else 0)
+    p = qt._params
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, qt._qdata), sa, p.scale, b, out_dtype=compute_dtype)
+    assert torch.equal(y.reshape(-1, N).cpu().view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("weight_format,opts", [("fp8", {}), ("int4", {"group_size": 128})])
+@pytest.mark.parametrize("M", [1, 40, 300])
+def test_fp8_int4_quantlinear(gpu, weight_format, opts, M):
+    K, N = 1024, 640
+    layer, qt, b = make_layer(K, N, weight_format, opts, torch.bfloat16, True, gpu, seed=21 + M)
+    x = heavy_rows(M, K, seed=22 + M, dtype=torch.bfloat16, outlier_frac=0 if weight_format == "int4" else 0.01)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        y = layer(x.to(gpu))
+    assert layer._ps_native
+    p = qt._params
+    if weight_format == "fp8":
+        qa, sa = oracle.quantize_rows_fp8(x)
+        ref = oracle.gemm_fp8(qa, sa, qt._qdata.view(torch.uint8), p.scale, b)
+    else:
+        wd = oracle.dequant_uint4(qt._qdata, p.scale, p.zero, p.group_size)
+        ref = oracle.gemm_wonly(x, wd, None, b)
+    within_fp32_bar(y, ref)
+
+
+@pytest.mark.parametrize("weight_format,opts", [("int8", {"convrot": True, "convrot_groupsize": 256}),
+                                                ("fp8", {}), ("int4", {"group_size": 128})])
+def test_dequantize_mode_matches_dequantized_linear(gpu, weight_format, opts):
+    """compute='dequantize': F.linear(rows, qt.dequantize().to(dtype), bias) (quant_linear.py:219-220),
+    with the GPU decoders bit-identical to the oracle's, so the torch GEMM sees the same weight."""
+    K, N, M = 512, 384, 70
+    layer, qt, b = make_layer(K, N, weight_format, opts, torch.bfloat16, False, gpu, seed=31)
+    x = heavy_rows(M, K, seed=32, dtype=torch.bfloat16)
+    y = layer(x.to(gpu))
+    assert not layer._ps_native
+    p = qt._params
+    if weight_format == "int8":
+        wd = oracle.dequant_i8_rows(qt._qdata, p.scale, 256, out_dtype=torch.bfloat16)
+    elif weight_format == "fp8":
+        wd = oracle.dequant_fp8(qt._qdata.view(torch.uint8), p.scale, out_dtype=torch.bfloat16)
+    else:
+        wd = oracle.dequant_uint4(qt._qdata, p.scale, p.zero, p.group_size, out_dtype=torch.bfloat16)
+    ref = torch.nn.functional.linear(x.to(gpu), wd.to(gpu), b.to(gpu))
+    assert torch.equal(y, ref)
+
+
+def test_unsupported_shape_warns_and_dequantizes(gpu):
+    """K = 960 quantizes but is not a whole number of 128-byte GEMM stages: the native GEMM reports
+    PSQ_E_SHAPE -> RuntimeError -> one warning, the module switches to dequantize for good."""
+    K, N, M = 960, 256, 33
+    layer, qt, b = make_layer(K, N, "int8", {"convrot": False}, torch.bfloat16, True, gpu, seed=41)
+    x = heavy_rows(M, K, seed=42, dtype=torch.bfloat16)
+    with pytest.warns(UserWarning, match="switches to dequantize"):
+        y = layer(x.to(gpu))
+    assert not layer._ps_native
+    wd = oracle.dequant_i8_rows(qt._qdata, qt._params.scale, 0, out_dtype=torch.bfloat16)
+    ref = torch.nn.functional.linear(x.to(gpu), wd.to(gpu), b.to(gpu))
+    assert torch.equal(y, ref)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")      # no second warning
+        layer(x.to(gpu))
+
+
+def test_follow_input_returns_input_dtype(gpu):
+    """Text-encoder install (follow_input=True, native_te.py:370-372): an fp32 graph gets fp32 back,
+    computed by the bf16 native path (quant_linear.py:221-223)."""
+    K, N, M = 512, 256, 9
+    layer, qt, b = make_layer(K, N, "int8", {"convrot": True, "convrot_groupsize": 256}, torch.bfloat16, True, gpu,
+                              seed=51, follow_input=True)
+    x = heavy_rows(M, K, seed=52).float()
+    y = layer(x.to(gpu))
+    assert y.dtype == torch.float32 and layer._ps_native
+    qa, sa = oracle.quantize_rows_i8(x.to(torch.bfloat16), 256)
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, qt._qdata), sa, qt._params.scale, b)
+    assert torch.equal(y.cpu(), ref.float())
