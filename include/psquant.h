@@ -69,7 +69,7 @@ PSQ_API int psq_device_supported(int device);
  *          (the module's input_scale, powershard/quant_linear.py:28-30)
  *   q      [M, K] int8 / e4m3fn codes, row stride ldq bytes
  *   scale  [M] fp32 per-row scale (s = absmax/127 or absmax/448; 0 -> 1)
- * K must be a multiple of 16 and at most 16384.  Bit-exact with the oracle. */
+ * K must be a multiple of 16 and at most 32768.  Bit-exact with the oracle. */
 PSQ_API int psq_quantize_rows_i8(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                          int rot_group, const float *static_scale, int8_t *q, int64_t ldq,
                          float *scale, void *stream);
@@ -106,7 +106,7 @@ PSQ_API int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, co
  * (powershard/quant_linear.py:239, weight-only formats) and matches the dequantize
  * branch F.linear(rows, qt.dequantize().to(bf16), bias) (quant_linear.py:219-220).
  *   x [M, K] bf16 (ldx), wq [N, K/2] bytes (low nibble = even k), scale/zero [N, K/group]
- *   fp16, group_size in {32, 64, 128, 256, ...} multiple of 32 dividing K. */
+ *   fp16, group_size a multiple of 64 dividing K. */
 PSQ_API int psq_gemm_w4a16(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq,
                    const uint16_t *w_scale, const uint16_t *w_zero, int group_size,
                    const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,

@@ -49,7 +49,7 @@ def _fake(addr=0x10000):
     # rotation group not a power of 4
     (lambda L: L.psq_quantize_rows_i8(_fake(), 0, 4, 512, 512, 128, None, _fake(), 512, _fake(), None), -2),
     # K beyond the per-row kernel
-    (lambda L: L.psq_quantize_rows_i8(_fake(), 0, 4, 65552, 65552, 0, None, _fake(), 65552, _fake(), None), -2),
+    (lambda L: L.psq_quantize_rows_i8(_fake(), 0, 4, 32784, 32784, 0, None, _fake(), 32784, _fake(), None), -2),
     # fp32 activations are not accepted by the quantizer
     (lambda L: L.psq_quantize_rows_fp8(_fake(), 2, 4, 512, 512, 0, None, _fake(), 512, _fake(), None), -1),
     # uint4 group size must be a multiple of 64 for the GEMM

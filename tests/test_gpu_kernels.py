@@ -88,6 +88,13 @@ QUANT_CASES = [
     (8, 4096, 4, torch.float16),
     (1, 16, 0, torch.bfloat16),
     (300, 2048, 256, torch.bfloat16),
+    # two 16-element chunks per thread (K > 16384): Qwen3-VL down_proj K, the maximum, just over
+    (7, 25600, 256, torch.bfloat16),
+    (3, 32768, 1024, torch.float16),
+    (5, 16400, 16, torch.bfloat16),
+    # more rows than resident workgroups: each workgroup streams several rows
+    (20000, 1024, 256, torch.bfloat16),
+    (33000, 256, 64, torch.float16),
 ]
 
 
