@@ -34,7 +34,10 @@ namespace {
 constexpr int BM = 256, BN = 256, BK = 64;    // BK in bytes (= elements for int8/fp8)
 // LDS ring depth (NSTAGE - 1 stages in flight): 4 for int8; 3 for fp8, whose fragment sets
 // alternate per stage and so need an even number of stages between tile switches.
-template <bool FP8> constexpr int ring_depth() { return FP8 ? 3 : 4; }
+#ifndef PSQ_Q8_RING_I8
+#define PSQ_Q8_RING_I8 4
+#endif
+template <bool FP8> constexpr int ring_depth() { return FP8 ? 3 : PSQ_Q8_RING_I8; }
 constexpr int NTHREADS = 256;                  // 4 waves, one per SIMD
 constexpr int WAVE_M = 128, WAVE_N = 128;
 constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;   // 4 x 4 MFMA tiles of 32 x 32 per wave
@@ -197,7 +200,9 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     constexpr bool SCALED = OUT != OUT_I32;
     constexpr int NSTAGE = ring_depth<FP8>();
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave-uniform values in scalar registers: the LDS destination of every global->LDS load (M0)
+    // is then computed without a VALU -> SGPR round trip
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
     int v, step, vend;
@@ -213,19 +218,27 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     // of a tile they fetch the first stages of the workgroup's next tile (pointer set `nx`); after
     // its last tile a workgroup re-issues the tile's last stage, a load into a ring slot nobody
     // reads again, so every stage issues the same number of loads and the waits are static.
-    struct Ptrs { const uint8_t *a[LOADS], *w[LOADS]; };
-    Ptrs cu;                                  // the current tile's rows
-    int64_t da[LOADS] = {}, dw[LOADS] = {};   // next tile's rows minus the current tile's
-    auto point_at = [&](int tv, int buf, Ptrs &p) {
+    // A tile's rows are addressed as a wave-uniform base (A + m0 lda, W + n0 ldw: scalar
+    // registers) plus a per-lane 32-bit offset -- the scalar-base form of global_load_lds, so a
+    // load costs no 64-bit vector address arithmetic.  Rows past M (N) are clamped to the last
+    // row; the tile's stores skip them.
+    const uint8_t *ba = nullptr, *bw = nullptr;       // current tile
+    const uint8_t *nba = nullptr, *nbw = nullptr;     // next tile
+    uint32_t oa[LOADS], ow[LOADS];                    // current tile's lane offsets
+    int32_t doa[LOADS] = {}, dow[LOADS] = {};         // next tile's offsets minus the current ones
+    auto point_at = [&](int tv, int buf, const uint8_t *&pa, const uint8_t *&pw, uint32_t (&qa)[LOADS],
+                        uint32_t (&qw)[LOADS]) {
         int m0, n0;
         tile_coords(tv, nbm, nbn, m0, n0);
+        pa = A + (int64_t)m0 * lda;
+        pw = W + (int64_t)n0 * ldw;
 #pragma unroll
         for (int j = 0; j < LOADS; j++) {
             const int b = j * (NTHREADS / 64) + wave;
             const int r = 16 * b + (lane >> 2);
             const int c = (lane & 3) ^ (FP8 ? (((r >> 1) & 1) << 1) : swz_i8(r));
-            p.a[j] = A + (int64_t)min(m0 + r, M - 1) * lda + c * 16;
-            p.w[j] = W + (int64_t)min(n0 + r, N - 1) * ldw + c * 16;
+            qa[j] = (uint32_t)(min(r, M - 1 - m0) * lda + c * 16);
+            qw[j] = (uint32_t)(min(r, N - 1 - n0) * ldw + c * 16);
         }
         if constexpr (SCALED) {
             // the tile's row scales, column scales and bias words: 64 entries of each per wave
@@ -241,16 +254,16 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         }
     };
     // ring load q of a stage (q < LOADS: A block q, else W block q - LOADS), from the current tile
-    // (same) or the next one, at byte offset koff along K, into ring slot `slot`
-    // (the next tile's address is formed by adding a masked delta, not by selecting between two
-    // pointer sets: a select of pointers gets turned into a load from a selected address, which
-    // sends both sets to scratch memory)
+    // (same) or the next one, at byte offset koff along K, into ring slot `slot`.  The next tile's
+    // lane offset is the current one plus a masked delta (a select between two offset arrays is
+    // turned into a load from a selected address, which sends both arrays to scratch memory).
     auto issue_one = [&](int slot, bool same, int64_t koff, int q) {
         const int j = q % LOADS, b = j * (NTHREADS / 64) + wave;
         lds_ptr d = (lds_ptr)(smem + slot * 2 * STAGE_BYTES + (q < LOADS ? 0 : STAGE_BYTES) + 1024 * b);
-        const int64_t mask = same ? 0 : -1;
-        const uint8_t *g = q < LOADS ? cu.a[j] + (da[j] & mask) : cu.w[j] + (dw[j] & mask);
-        __builtin_amdgcn_global_load_lds((glb_ptr)(g + koff), d, 16, 0, 0);
+        const int32_t mask = same ? 0 : -1;
+        const uint8_t *base = (q < LOADS ? (same ? ba : nba) : (same ? bw : nbw)) + koff;
+        const uint32_t off = q < LOADS ? oa[j] + (uint32_t)(doa[j] & mask) : ow[j] + (uint32_t)(dow[j] & mask);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(base + off), d, 16, 0, 0);
     };
     auto issue_stage = [&](int slot, bool same, int64_t koff) {
 #pragma unroll
@@ -305,8 +318,20 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     constexpr int kSchedRead[16] = {0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7, -1};
     constexpr int kSchedLoadA[16] = {-1, 0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7};
     constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
-#else
+#elif PSQ_Q8_SCHED == 3
     constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
+    constexpr int kSchedLoadA[16] = {-1, -1, -1, 0, -1, -1, -1, 1, -1, -1, -1, 2, -1, -1, -1, 3};
+    constexpr int kSchedLoadB[16] = {-1, -1, -1, 4, -1, -1, -1, 5, -1, -1, -1, 6, -1, -1, -1, 7};
+#elif PSQ_Q8_SCHED == 4
+    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
+    constexpr int kSchedLoadA[16] = {-1, -1, -1, -1, -1, -1, -1, -1, 0, -1, 1, -1, 2, -1, 3, -1};
+    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, 4, -1, 5, -1, 6, -1, 7, -1};
+#elif PSQ_Q8_SCHED == 5
+    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
+    constexpr int kSchedLoadA[16] = {-1, 0, -1, -1, -1, 1, -1, -1, -1, 2, -1, -1, -1, 3, -1, -1};
+    constexpr int kSchedLoadB[16] = {-1, 4, -1, -1, -1, 5, -1, -1, -1, 6, -1, -1, -1, 7, -1, -1};
+#else
+    constexpr int kSchedRead[16] = {0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7, -1};
     constexpr int kSchedLoadA[16] = {-1, -1, -1, 0, -1, -1, -1, 1, -1, -1, -1, 2, -1, -1, -1, 3};
     constexpr int kSchedLoadB[16] = {-1, -1, -1, 4, -1, -1, -1, 5, -1, -1, -1, 6, -1, -1, -1, 7};
 #endif
@@ -445,7 +470,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     };
 
     // ---------------------------------------------------------------- main loop
-    point_at(v, 0, cu);
+    point_at(v, 0, ba, bw, oa, ow);
 #pragma unroll
     for (int s = 0; s < NSTAGE - 1; s++) issue_stage(s, true, (int64_t)min(s, nk - 1) * BK);
     wait_vmcnt<(NSTAGE - 2) * LPS>();
@@ -517,12 +542,12 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         tile_coords(v, nbm, nbn, m0, n0);
         has_next = v + step < vend;
         if (has_next) {
-            Ptrs nx;
-            point_at(v + step, buf == NSCALEBUF - 1 ? 0 : buf + 1, nx);
+            uint32_t qa[LOADS], qw[LOADS];
+            point_at(v + step, buf == NSCALEBUF - 1 ? 0 : buf + 1, nba, nbw, qa, qw);
 #pragma unroll
             for (int j = 0; j < LOADS; j++) {
-                da[j] = nx.a[j] - cu.a[j];
-                dw[j] = nx.w[j] - cu.w[j];
+                doa[j] = (int32_t)(qa[j] - oa[j]);
+                dow[j] = (int32_t)(qw[j] - ow[j]);
             }
         }
 #pragma unroll
@@ -546,10 +571,12 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         epilogue(m0, n0, buf);
         buf = buf == NSCALEBUF - 1 ? 0 : buf + 1;
         if (has_next) {
+            ba = nba;
+            bw = nbw;
 #pragma unroll
             for (int j = 0; j < LOADS; j++) {
-                cu.a[j] += da[j];
-                cu.w[j] += dw[j];
+                oa[j] += (uint32_t)doa[j];
+                ow[j] += (uint32_t)dow[j];
             }
         }
     }
@@ -623,6 +650,8 @@ int check_shapes(const char *name, const void *a, int64_t lda, const void *w, in
     if (((uintptr_t)a & 15) || ((uintptr_t)w & 15)) return set_error(PSQ_E_SHAPE, "%s: operands must be 16-byte aligned", name);
     if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 30))
         return set_error(PSQ_E_SHAPE, "%s: size too large", name);
+    if (lda > (1LL << 23) || ldw > (1LL << 23))   // a tile's row offsets (256 rows) fit in 31 bits
+        return set_error(PSQ_E_SHAPE, "%s: lda/ldw above 2^23", name);
     return PSQ_OK;
 }
 
