@@ -28,7 +28,7 @@ INCLUDE = PKG.parent.parent / "include"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 CFLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++20",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fvisibility=hidden", "-Wall", "-Wno-unused-function", f"-I{INCLUDE}",

@@ -76,9 +76,6 @@ __device__ __forceinline__ void store1(void *p, int c, float v)
 // LDS: the K-loop ring, then the epilogue operands.
 constexpr size_t kRingBytes = 4 * 2 * STAGE_BYTES;   // the deeper (int8) ring
 
-typedef __attribute__((address_space(3))) uint8_t *lds_ptr;
-typedef const __attribute__((address_space(1))) void *glb_ptr;
-
 // Stage rows are 64 bytes = four 16-byte chunks; a 32-lane MFMA fragment read touches 32
 // consecutive rows at one logical chunk.  int8 stores chunk ^ x(row) with x = (r1 ^ r3, r2) (bits
 // of the row): bijective in (r1, r2) and in (r2, r3), so both 8 consecutive rows (a 32-bank,
@@ -101,23 +98,6 @@ __device__ __forceinline__ int swz(int row, int chunk)
 {
     const int x = FP8 ? (((row >> 1) & 1) << 1) : swz_i8(row);
     return row * BK + ((chunk ^ x) << 4);
-}
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4]<<14)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt()
-{
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier for the K loop.  __syncthreads() carries a workgroup fence, which makes the
-// compiler drain every outstanding global->LDS load (vmcnt(0)) -- including the stages just put
-// in flight.  The loop instead waits explicitly for the stage it needs (wait_vmcnt) and for its
-// own LDS reads (lgkmcnt(0)), then meets the other waves; the asm memory clobber keeps the
-// compiler from moving LDS accesses across the barrier.
-__device__ __forceinline__ void stage_barrier()
-{
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 template <bool FP8> struct Frag;
@@ -155,23 +135,6 @@ __device__ __forceinline__ void tile_coords(int v, int nbm, int nbn, int &m0, in
     const int r = v - g * per_group;
     m0 = (first + r % h) * BM;
     n0 = (r / h) * BN;
-}
-
-// Reads an accumulator element through an AGPR operand.  The epilogue's arithmetic cannot take
-// AGPRs, and left to itself the register allocator then keeps the whole accumulator array in
-// VGPRs (and spills everything else); reading each element with an explicit AGPR-to-VGPR move
-// keeps the accumulators in the AGPR file for the MFMAs.
-__device__ __forceinline__ int agpr_read(int a)
-{
-    int v;
-    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
-    return v;
-}
-__device__ __forceinline__ int agpr_read(float a)
-{
-    int v;
-    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
-    return v;
 }
 
 // Bias word (see above) to fp32.

@@ -1,5 +1,5 @@
 // gemm_wonly.hip -- weight-only quantized GEMMs: uint4 asymmetric groups (W4A16) and int8 rows
-// (W8A16), dequantized in registers and fed to the bf16 / f16 MFMA (v_mfma_f32_16x16x32_*).
+// (W8A16), dequantized in registers and fed to the bf16 / f16 MFMA.
 //
 // W4A16 reproduces the dequantize branch of QuantLinear.forward,
 //   F.linear(rows, qt.dequantize().to(bf16), bias)   (powershard/quant_linear.py:219-220),
@@ -8,34 +8,17 @@
 // W8A16: int8 values are exact in bf16, the per-row scale is applied in the epilogue,
 // y = round_out(fmaf(acc, s[n], bias[n])) (Int8Linear storage, powershard/operations.py:96-132).
 //
-// Tiling: 128 x 128 output tile per workgroup of 4 waves (2 x 2, wave tile 64 x 64 = 4 x 4
-// MFMA tiles), K in stages of 64 elements double-buffered in LDS: activations as 128-byte
-// rows (XOR-swizzled 16-byte chunks), packed weights as padded rows (bank-conflict free
-// 4/8-byte fragment reads), group scale and zero per weight row and stage.
+// Two kernels: a weight-streaming one for M <= 64 (decode / short prompts: HBM-bound) and a
+// 256 x 256-tile one for larger M (MFMA-bound), both described where they are defined.
 #include "psq_common.hpp"
 
 namespace psq {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64;     // BK in elements
 constexpr int NTHREADS = 256;
-constexpr int WAVE_M = 64, WAVE_N = 64;
-constexpr int TM = WAVE_M / 16, TN = WAVE_N / 16;
-constexpr int XROW = BK * 2;                   // bytes per activation row in LDS (128)
-constexpr int X_STAGE = BM * XROW;             // 16 KB
-constexpr int GROUP_M = 4;
+constexpr int KSTAGE = 64;                     // K granularity of every path
 
 enum { W_UINT4 = 0, W_INT8 = 1 };
-
-template <int WK> struct WTraits;
-template <> struct WTraits<W_UINT4> {
-    static constexpr int ROW_BYTES = BK / 2;     // 32 bytes of packed nibbles per row per stage
-    static constexpr int PITCH = 36;             // padded LDS pitch (9 words: conflict free)
-};
-template <> struct WTraits<W_INT8> {
-    static constexpr int ROW_BYTES = BK;         // 64 bytes per row per stage
-    static constexpr int PITCH = 72;             // padded LDS pitch (18 words)
-};
 
 struct WArgs {
     const uint8_t *wq;          // uint4 [N, K/2] or int8 [N, K]
@@ -50,174 +33,10 @@ struct WArgs {
     int64_t ldy;
 };
 
-__device__ __forceinline__ int xswz(int row, int chunk) { return row * XROW + ((chunk ^ (row & 7)) << 4); }
-
 template <int XDT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi)
 {
     return pack_half2<XDT>(lo, hi);
-}
-
-template <int XDT, int WK>
-__global__ void __launch_bounds__(NTHREADS, 2)
-gemm_wonly_kernel(const uint16_t *__restrict__ X, int64_t ldx, int M, int N, int K, WArgs wa)
-{
-    using WT = WTraits<WK>;
-    __shared__ __attribute__((aligned(16))) uint8_t sx[2][X_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sw[2][BN * WT::PITCH];
-    __shared__ float2 ssz[2][BN];     // uint4: (scale, zero) of the stage's group per row
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
-    int pm, pn;
-    tile_order(blockIdx.x, nbm, nbn, GROUP_M, pm, pn);
-    const int m0 = pm * BM, n0 = pn * BN;
-
-    // activations: 128 rows x 8 chunks = 1024 chunks, 4 per thread
-    const int xchunk = tid & 7;
-    const uint16_t *px[4];
-    int xoff[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int r = (tid >> 3) + 32 * j;
-        px[j] = X + (int64_t)min(m0 + r, M - 1) * ldx + xchunk * 8;
-        xoff[j] = xswz(r, xchunk);
-    }
-    // weights: uint4 -> 128 rows x 2 chunks (1 per thread); int8 -> 128 rows x 4 chunks (2 per thread)
-    constexpr int WCH = WT::ROW_BYTES / 16;            // 16-byte chunks per row per stage
-    constexpr int WLOADS = BN * WCH / NTHREADS;
-    const uint8_t *pw[WLOADS];
-    int woff[WLOADS];
-    const int64_t wrow_bytes = (WK == W_UINT4) ? (int64_t)K / 2 : (int64_t)K;
-#pragma unroll
-    for (int j = 0; j < WLOADS; j++) {
-        const int id = tid + j * NTHREADS;
-        const int r = id / WCH, c = id % WCH;
-        pw[j] = wa.wq + (int64_t)min(n0 + r, N - 1) * wrow_bytes + c * 16;
-        woff[j] = r * WT::PITCH + c * 16;
-    }
-    const int G = (WK == W_UINT4) ? K / wa.gs : 1;
-    const int szrow = min(n0 + tid, N - 1);
-
-    v4f acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    v4i rx[4], rw[WLOADS];
-    float rs = 0.f, rz = 0.f;
-    auto gload = [&](int kt) {
-        const int64_t k0 = (int64_t)kt * BK;
-#pragma unroll
-        for (int j = 0; j < 4; j++) rx[j] = *(const v4i *)(px[j] + k0);
-#pragma unroll
-        for (int j = 0; j < WLOADS; j++)
-            rw[j] = *(const v4i *)(pw[j] + (WK == W_UINT4 ? k0 / 2 : k0));
-        if constexpr (WK == W_UINT4) {
-            if (tid < BN) {
-                const int64_t gi = (int64_t)szrow * G + k0 / wa.gs;
-                rs = f16_to_f32(wa.scale16[gi]);
-                rz = f16_to_f32(wa.zero16[gi]);
-            }
-        }
-    };
-    auto sstore = [&](int st) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) *(v4i *)(&sx[st][xoff[j]]) = rx[j];
-#pragma unroll
-        for (int j = 0; j < WLOADS; j++) {
-            // padded pitch is not 16-byte aligned for every row: store as dwords
-            uint32_t *d = (uint32_t *)(&sw[st][woff[j]]);
-            d[0] = rw[j][0]; d[1] = rw[j][1]; d[2] = rw[j][2]; d[3] = rw[j][3];
-        }
-        if constexpr (WK == W_UINT4) {
-            if (tid < BN) ssz[st][tid] = make_float2(rs, rz);
-        }
-    };
-
-    const int nk = K / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-
-    const int frow = lane & 15, fk = lane >> 4;
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
-#pragma unroll
-        for (int ks = 0; ks < BK / 32; ks++) {
-            v8bf fx[TM];
-            v8bf fwv[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                v4i t = *(const v4i *)(&sx[cur][xswz(wm * WAVE_M + i * 16 + frow, ks * 4 + fk)]);
-                fx[i] = __builtin_bit_cast(v8bf, t);
-            }
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int r = wn * WAVE_N + j * 16 + frow;   // weight row (output column)
-                uint32_t h[4];
-                if constexpr (WK == W_UINT4) {
-                    // 8 nibbles of k = ks*32 + fk*8 + 0..7, low nibble first
-                    const uint32_t p = *(const uint32_t *)(&sw[cur][r * WT::PITCH + ks * 16 + fk * 4]);
-                    const float2 sz = ssz[cur][r];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const float q0 = (float)((p >> (8 * e)) & 15u);
-                        const float q1 = (float)((p >> (8 * e + 4)) & 15u);
-                        h[e] = pack2<XDT>((q0 - sz.y) * sz.x, (q1 - sz.y) * sz.x);
-                    }
-                } else {
-                    const uint32_t *src = (const uint32_t *)(&sw[cur][r * WT::PITCH + ks * 32 + fk * 8]);
-                    const uint32_t p0 = src[0], p1 = src[1];
-#pragma unroll
-                    for (int e = 0; e < 2; e++) {
-                        const uint32_t p = e ? p1 : p0;
-                        const float q0 = (float)(int8_t)(p & 0xffu);
-                        const float q1 = (float)(int8_t)((p >> 8) & 0xffu);
-                        const float q2 = (float)(int8_t)((p >> 16) & 0xffu);
-                        const float q3 = (float)(int8_t)(p >> 24);
-                        h[2 * e] = pack2<XDT>(q0, q1);
-                        h[2 * e + 1] = pack2<XDT>(q2, q3);
-                    }
-                }
-                v4i t = {(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
-                fwv[j] = __builtin_bit_cast(v8bf, t);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    if constexpr (XDT == PSQ_BF16)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fx[i], fwv[j], acc[i][j], 0, 0, 0);
-                    else
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, fx[i]),
-                                                                           __builtin_bit_cast(v8h, fwv[j]),
-                                                                           acc[i][j], 0, 0, 0);
-                }
-        }
-        if (kt + 1 < nk) sstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    const int rbase = m0 + wm * WAVE_M + (lane >> 4) * 4;
-    const int cbase = n0 + wn * WAVE_N + (lane & 15);
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-        const int n = cbase + j * 16;
-        const int nc = min(n, N - 1);
-        const float cs = (WK == W_INT8) ? wa.scale32[nc] : 1.0f;
-        const float b = wa.bias ? load_elem(wa.bias, nc, wa.bias_dtype) : 0.0f;
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int m = rbase + i * 16 + v;
-                if (m < M && n < N) store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype, __builtin_fmaf(acc[i][j][v], cs, b));
-            }
-    }
 }
 
 // Skinny weight-only GEMM (M <= 64, the decode / text-encoder shapes, bound by the weight stream):
@@ -229,6 +48,25 @@ gemm_wonly_kernel(const uint16_t *__restrict__ X, int64_t ldx, int M, int N, int
 // operands use the same assignment, so every dot product is complete.  The four waves' partial
 // tiles are added through LDS in a fixed order, then the epilogue of the tiled kernel applies.
 constexpr int SK_BLOCK = 128;                  // k per block: 4 lane groups x 32
+
+// The four bytes of w as floats: v_cvt_f32_ubyte0..3, one instruction each (the compiler would
+// otherwise extract each nibble-masked byte with a bitfield op first).
+__device__ __forceinline__ float ubyte_to_f32(uint32_t w, int e)
+{
+    float f;
+    if (e == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(w));
+    else if (e == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(w));
+    else if (e == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(w));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(w));
+    return f;
+}
+__device__ __forceinline__ void ubytes_to_f32(uint32_t w, float (&f)[4])
+{
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f[0]) : "v"(w));
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f[1]) : "v"(w));
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f[2]) : "v"(w));
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f[3]) : "v"(w));
+}
 
 template <int XDT, int WK, int MT>
 __global__ void __launch_bounds__(NTHREADS)
@@ -256,7 +94,16 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
     // The weight stream is software-pipelined one block deep (the next block's words and group
     // scale / zero load while this block computes); the activation fragments, L2 hits, load at the
     // top of each block.
-    struct WBlock { uint32_t w[NW]; float s, z; };
+    // Activation fragments of MT <= 2 row tiles ride in the same pipeline (they are L2 hits, but
+    // their latency would otherwise be exposed once per block).
+    constexpr bool XPRE = MT <= 2;
+    struct WBlock { uint32_t w[NW]; float s, z; v4i x[XPRE ? 4 : 1][XPRE ? MT : 1]; };
+    auto load_x = [&](int kb, v4i (&xv)[4][MT]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) xv[t][mt] = *(const v4i *)(xrow[mt] + kb + 8 * t);
+    };
     auto load_w = [&](int b, WBlock &r) {
         const int kb = b * SK_BLOCK + 32 * h;
         const v4i t0 = *(const v4i *)(wrow + kb / WROW_DIV);
@@ -273,14 +120,16 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
             r.s = f16_to_f32(wa.scale16[gi]);
             r.z = f16_to_f32(wa.zero16[gi]);
         }
+        if constexpr (XPRE) load_x(kb, r.x);
     };
     auto compute = [&](int b, const WBlock &r) {
         const int kb = b * SK_BLOCK + 32 * h;        // the lane group's first k
-        v4i xv[4][MT];
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) xv[t][mt] = *(const v4i *)(xrow[mt] + kb + 8 * t);
+        v4i xl[4][MT];
+        if constexpr (!XPRE) load_x(kb, xl);
+        auto xfrag = [&](int t, int mt) -> v4i {
+            if constexpr (XPRE) return r.x[t][mt];
+            else return xl[t][mt];
+        };
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             // weights of k = kb + 8t .. kb + 8t + 7
@@ -288,12 +137,11 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
             if constexpr (WK == W_UINT4) {
                 const uint32_t p = r.w[t];
                 const uint32_t lo = p & 0x0f0f0f0fu, hi = (p >> 4) & 0x0f0f0f0fu;   // even / odd k
+                float q0[4], q1[4];
+                ubytes_to_f32(lo, q0);
+                ubytes_to_f32(hi, q1);
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float q0 = (float)((lo >> (8 * e)) & 0xffu);
-                    const float q1 = (float)((hi >> (8 * e)) & 0xffu);
-                    hw[e] = pack2<XDT>((q0 - r.z) * r.s, (q1 - r.z) * r.s);
-                }
+                for (int e = 0; e < 4; e++) hw[e] = pack2<XDT>((q0[e] - r.z) * r.s, (q1[e] - r.z) * r.s);
             } else {
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
@@ -305,7 +153,7 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
             const XV wf = __builtin_bit_cast(XV, v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]});
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const XV xf = __builtin_bit_cast(XV, xv[t][mt]);
+                const XV xf = __builtin_bit_cast(XV, xfrag(t, mt));
                 if constexpr (XDT == PSQ_BF16)
                     acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xf, acc[mt], 0, 0, 0);
                 else
@@ -338,6 +186,298 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
     }
 }
 
+// ------------------------------------------------------------------ tiled kernel (M > 64)
+// A 256 x 256 output tile per workgroup of 4 waves.  Wave w owns all 256 rows (tokens) and the
+// 64 weight rows (output columns) 64w .. 64w + 63: 8 x 2 MFMA tiles of 32 x 32 on
+// v_mfma_f32_32x32x16_bf16 / f16 with the accumulators in AGPRs.  So every weight element is
+// dequantized once per workgroup, by the one wave that multiplies it, for 256 rows.  K runs in
+// stages of 64 through a 3-deep LDS ring filled by global->LDS loads: per stage the activations
+// (256 rows x 128 bytes, XOR-swizzled 16-byte chunks), the packed weights (256 rows x 32 bytes of
+// nibbles, or 64 bytes of int8) and, for uint4, each weight row's group scale and zero (one
+// 32-bit word each, zero-extended fp16).  Inside a stage the MFMAs of k-step t run beside the
+// activation fragment reads and the weight dequantization of k-step t + 1; the stage's one
+// barrier sits before its last k-step, whose MFMAs cover the next stage's first reads and
+// dequantization.  Lane-half h of every fragment carries k = 32 h + 8 t .. + 7 of the stage in
+// k-step t, for both operands, so a lane's weights of a stage are 16 contiguous bytes of nibbles.
+namespace wt {
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int NSTAGE = 3;                          // two stages in flight
+constexpr int TM = 8, TN = 2;                      // 32 x 32 tiles per wave: 256 rows x 64 columns
+constexpr int XROW = BK * 2;                       // activation bytes per row per stage
+constexpr int XBYTES = BM * XROW;                  // 32 KB
+constexpr int XDMA = XBYTES / 1024 / 4;            // activation loads per wave per stage (8)
+template <int WK> constexpr int wrow() { return WK == W_UINT4 ? BK / 2 : BK; }         // 32 / 64 B
+template <int WK> constexpr int wdma() { return BN * wrow<WK>() / 1024 / 4; }          // 2 / 4
+template <int WK> constexpr int szdma() { return WK == W_UINT4 ? 2 : 0; }
+template <int WK> constexpr int lps() { return XDMA + wdma<WK>() + szdma<WK>(); }      // 12 / 12
+template <int WK> constexpr int slot_bytes() { return XBYTES + BN * wrow<WK>() + (WK == W_UINT4 ? 2 * BN * 4 : 0); }
+template <int WK> constexpr int lds_bytes() { return NSTAGE * slot_bytes<WK>(); }      // 126 / 144 KB
+// activation chunk swizzle: bijective on 8 consecutive rows (32 banks) and on each parity class
+// of 16 consecutive rows (64 banks), so a fragment read (32 rows, one logical chunk) is conflict free
+__device__ __forceinline__ int xsw(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
+}  // namespace wt
+
+template <int XDT, int WK>
+__global__ void __launch_bounds__(NTHREADS, 1)
+gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
+{
+    using namespace wt;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
+    constexpr int LPS = lps<WK>();
+    constexpr int RB = wrow<WK>();
+    constexpr int WDMA = wdma<WK>();
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int frow = lane & 31, h = lane >> 5;
+    const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
+    int pm, pn;
+    tile_order(blockIdx.x, nbm, nbn, 4, pm, pn);
+    const int m0 = pm * BM, n0 = pn * BN;
+    const int nk = K / BK;
+    const int G = WK == W_UINT4 ? K / wa.gs : 1;
+    const int64_t wld = WK == W_UINT4 ? K / 2 : K;          // weight row bytes
+
+    // ---- ring loads (scalar base + 32-bit lane offsets); rows past M / N clamp to the last row
+    uint32_t xo[XDMA], wo[WDMA];
+#pragma unroll
+    for (int j = 0; j < XDMA; j++) {
+        const int b = j * 4 + wave, r = 8 * b + (lane >> 3);
+        const int c = (lane & 7) ^ xsw(r);
+        xo[j] = (uint32_t)(min(r, M - 1 - m0) * ldx * 2 + c * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < WDMA; j++) {
+        const int b = j * 4 + wave;
+        const int per = 1024 / RB;                          // rows per load (32 / 16)
+        const int r = per * b + lane / (64 / per);
+        wo[j] = (uint32_t)(min(r, N - 1 - n0) * wld + (lane % (64 / per)) * 16);
+    }
+    const int scol = min(n0 + 64 * wave + lane, N - 1);      // scale / zero column of this lane
+    const unsigned spg = WK == W_UINT4 ? (unsigned)(wa.gs / BK) : 1u;   // stages per group
+    const uint8_t *xb = (const uint8_t *)(x + (int64_t)m0 * ldx);
+    const uint8_t *wb = wa.wq + (int64_t)n0 * wld;
+    // load q of a stage (q < 8: activation block q; then weight blocks; then, for uint4, the
+    // stage's scale and zero words of the wave's 64 columns)
+    auto issue_one = [&](int slot, int kt, auto qc) {
+        constexpr int q = decltype(qc)::value;
+        uint8_t *sl = smem + slot * slot_bytes<WK>();
+        if constexpr (q < XDMA) {
+            constexpr int b4 = q * 4;
+            __builtin_amdgcn_global_load_lds((glb_ptr)(xb + (int64_t)kt * BK * 2 + xo[q]),
+                                             (lds_ptr)(sl + 1024 * (b4 + wave)), 16, 0, 0);
+        } else if constexpr (q < XDMA + WDMA) {
+            constexpr int j = q - XDMA;
+            __builtin_amdgcn_global_load_lds((glb_ptr)(wb + (int64_t)kt * RB + wo[j]),
+                                             (lds_ptr)(sl + XBYTES + 1024 * (j * 4 + wave)), 16, 0, 0);
+        } else if constexpr (WK == W_UINT4) {
+            constexpr bool zero = q == LPS - 1;
+            const int64_t gi = (int64_t)scol * G + (int)((unsigned)kt / spg);   // the stage's group
+            __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
+                                             (lds_ptr)(sl + XBYTES + BN * RB + (zero ? BN * 4 : 0) + 256 * wave), 2, 0,
+                                             0);
+        }
+    };
+    auto issue_all = [&](int slot, int kt) {
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            (issue_one(slot, kt, std::integral_constant<int, Q>{}), ...);
+        }(std::make_integer_sequence<int, LPS>{});
+    };
+
+    // ---- fragments
+    auto read_x = [&](int slot, int t, int i) -> XV {
+        const int r = 32 * i + frow, c = 4 * h + t;
+        return __builtin_bit_cast(XV, *(const v4i *)(smem + slot * slot_bytes<WK>() + r * XROW + ((c ^ xsw(r)) << 4)));
+    };
+    // the lane's packed weights of a stage (its 32 k of each of its two columns) and, for uint4,
+    // the columns' group scale and zero
+    struct WRaw { v4i w[TN][RB / 32]; float s[TN], z[TN]; };
+    auto read_w = [&](int slot, WRaw &r) {
+        const uint8_t *sl = smem + slot * slot_bytes<WK>() + XBYTES;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = 64 * wave + 32 * j + frow;
+#pragma unroll
+            for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
+            if constexpr (WK == W_UINT4) {
+                r.s[j] = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
+                r.z[j] = f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n));
+            } else {
+                r.s[j] = 1.0f;
+                r.z[j] = 0.0f;
+            }
+        }
+    };
+    // pair e (k = 32 h + 8 t + 2e, +1) of column tile j's weights in k-step t, packed
+    auto dq_pair = [&](const WRaw &r, int j, int t, int e) -> uint32_t {
+        if constexpr (WK == W_UINT4) {
+            const uint32_t p = (uint32_t)r.w[j][0][t];
+            float q[2];
+            q[0] = ubyte_to_f32(p & 0x0f0f0f0fu, e);           // even k: low nibble of byte e
+            q[1] = ubyte_to_f32((p >> 4) & 0x0f0f0f0fu, e);    // odd k: high nibble
+            return pack2<XDT>((q[0] - r.z[j]) * r.s[j], (q[1] - r.z[j]) * r.s[j]);
+        } else {
+            const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
+            const int sh = 16 * (e & 1);
+            return pack2<XDT>((float)(int8_t)((p >> sh) & 0xffu), (float)(int8_t)((p >> (sh + 8)) & 0xffu));
+        }
+    };
+
+    v16f acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    auto mfma = [&](int i, int j, const XV &wf, const XV &xf) {
+        if constexpr (XDT == PSQ_BF16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf, acc[i][j], 0, 0, 0);
+        else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, xf, acc[i][j], 0, 0, 0);
+    };
+
+    // ---- prologue: stages 0 .. NSTAGE-2 in flight, stage 0 landed, its first fragments ready
+#pragma unroll
+    for (int st = 0; st < NSTAGE - 1; st++) issue_all(st, min(st, nk - 1));
+    wait_vmcnt<(NSTAGE - 2) * LPS>();
+    stage_barrier();
+    WRaw wr;
+    read_w(0, wr);
+    XV xa[TM], xb2[TM], wa0[TN], wb0[TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) xa[i] = read_x(0, 0, i);
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        uint32_t hw[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) hw[e] = dq_pair(wr, j, 0, e);
+        wa0[j] = __builtin_bit_cast(XV, v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]});
+    }
+
+    // One k-step: the 16 MFMAs of step t on (xc, wc); behind MFMA q the activation fragment
+    // q / 2 of the next step (even q), a weight pair of the next step (odd q: column tile
+    // q / 8, pair (q / 2) % 4), and for k-steps 0-2 a third of the stage's refill loads (q % 4 == 3).
+    // The instruction order is pinned: sched_barrier after every MFMA.
+    auto kstep = [&](auto tnc, auto basec, XV (&xc)[TM], XV (&wc)[TN], XV (&xn)[TM], XV (&wn)[TN], int xslot,
+                     const WRaw &wraw, int fill_slot, int fill_kt) {
+        constexpr int tn = decltype(tnc)::value, fill_base = decltype(basec)::value;
+        uint32_t hw[TN][4];
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            ([&] {
+                constexpr int q = Q;
+                mfma(q >> 1, q & 1, wc[q & 1], xc[q >> 1]);
+                if constexpr ((q & 1) == 0) xn[q >> 1] = read_x(xslot, tn, q >> 1);
+                else hw[q >> 3][(q >> 1) & 3] = dq_pair(wraw, q >> 3, tn, (q >> 1) & 3);
+                if constexpr (fill_base >= 0 && (q & 3) == 3)
+                    issue_one(fill_slot, fill_kt, std::integral_constant<int, fill_base + (q >> 2)>{});
+                __builtin_amdgcn_sched_barrier(0);
+            }(), ...);
+        }(std::make_integer_sequence<int, TM * TN>{});
+#pragma unroll
+        for (int j = 0; j < TN; j++) wn[j] = __builtin_bit_cast(XV, v4i{(int)hw[j][0], (int)hw[j][1], (int)hw[j][2], (int)hw[j][3]});
+    };
+    int rs = 0;
+#pragma clang loop unroll(disable)
+    for (int kt = 0; kt < nk; kt++) {
+        const int fill = rs == 0 ? NSTAGE - 1 : rs - 1;     // ring slot of stage kt + NSTAGE - 1
+        const int kfill = min(kt + NSTAGE - 1, nk - 1);      // (past the end: re-load the last stage)
+        const int nxt = rs == NSTAGE - 1 ? 0 : rs + 1;
+        using I = std::integral_constant<int, 0>;
+        kstep(std::integral_constant<int, 1>{}, I{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
+        kstep(std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{}, xb2, wb0, xa, wa0, rs, wr, fill, kfill);
+        kstep(std::integral_constant<int, 3>{}, std::integral_constant<int, 8>{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
+        // stage kt + 1 landed for every wave; nobody reads stage kt's slot any more
+        wait_vmcnt<(NSTAGE - 2) * LPS>();
+        stage_barrier();
+        read_w(nxt, wr);
+        kstep(I{}, std::integral_constant<int, -1>{}, xb2, wb0, xa, wa0, nxt, wr, 0, 0);
+        rs = nxt;
+    }
+    wait_vmcnt<0>();   // the re-issued tail loads land before the workgroup's LDS is released
+
+    // ---- epilogue: acc[i][j] is the transposed 32 x 32 tile, lane (l & 31) holds output row
+    // m = m0 + 32 i + (l & 31), register 4g + c column n = n0 + 64 wave + 32 j + 8 g + 4 h + c.
+    //   y = round_out(fmaf(acc, s[n], bias[n]))   (s = 1 for uint4)
+    const int nl0 = 64 * wave + 4 * h;                       // the lane's first column in the tile
+    const int esz = wa.y_dtype == PSQ_F32 ? 4 : 2;
+    uint8_t *rowp[TM];
+    bool live[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int m = m0 + 32 * i + frow;
+        live[i] = m < M;
+        rowp[i] = (uint8_t *)wa.y + ((int64_t)min(m, M - 1) * wa.ldy + n0 + nl0) * esz;
+    }
+    // operands of the lane's 4 columns n0 + nl0 + nc .. + 3: the row scale (int8) and the bias
+    auto operands = [&](int nc, float (&cs)[4], float (&bs)[4]) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int n = min(n0 + nl0 + nc + c, N - 1);
+            cs[c] = (WK == W_INT8) ? wa.scale32[n] : 1.0f;
+            bs[c] = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
+        }
+    };
+    auto value = [&](int i, int j, int r, float c, float b) {
+        return __builtin_fmaf(__int_as_float(agpr_read(acc[i][j][r])), c, b);
+    };
+    const bool fast = wa.y_dtype != PSQ_F32 && n0 + BN <= N && ((uintptr_t)wa.y & 15) == 0 && (wa.ldy * 2) % 16 == 0;
+    if (fast) {
+        // lanes l and l + 32 hold the same row: one v_permlane32_swap per word gives lane l columns
+        // 16 pr + 0..7 and lane l + 32 columns 16 pr + 8..15 of the column pair pr, one 16-byte store
+        const bool bf = wa.y_dtype == PSQ_BF16;
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int pr = 0; pr < 2; pr++) {
+                const int nc = 32 * j + 16 * pr;
+                float cs[2][4], bs[2][4];
+                operands(nc, cs[0], bs[0]);
+                operands(nc + 8, cs[1], bs[1]);
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    uint32_t x0[2], x1[2];
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        uint32_t *o = hh == 0 ? x0 : x1;
+                        const int r = 8 * pr + 4 * hh;
+                        const float v0 = value(i, j, r, cs[hh][0], bs[hh][0]), v1 = value(i, j, r + 1, cs[hh][1], bs[hh][1]);
+                        const float v2 = value(i, j, r + 2, cs[hh][2], bs[hh][2]), v3 = value(i, j, r + 3, cs[hh][3], bs[hh][3]);
+                        o[0] = bf ? pack_half2<PSQ_BF16>(v0, v1) : pack_half2<PSQ_F16>(v0, v1);
+                        o[1] = bf ? pack_half2<PSQ_BF16>(v2, v3) : pack_half2<PSQ_F16>(v2, v3);
+                    }
+                    uint32_t lo[2], hi[2];
+#pragma unroll
+                    for (int d = 0; d < 2; d++) {
+                        const auto sw = __builtin_amdgcn_permlane32_swap(x0[d], x1[d], false, false);
+                        lo[d] = sw[0];
+                        hi[d] = sw[1];
+                    }
+                    uint8_t *p = rowp[i] + (nc + 4 * h) * 2;
+                    if (live[i]) *(v4i *)p = v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    } else {
+        const int n_left0 = N - (n0 + nl0);
+        static_for<TN>([&](auto jc) {
+            static_for<4>([&](auto gc) {
+                constexpr int j = decltype(jc)::value, g = decltype(gc)::value, nc = 32 * j + 8 * g;
+                float cs[4], bs[4];
+                operands(nc, cs, bs);
+                static_for<TM>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    static_for<4>([&](auto cc) {
+                        constexpr int c = decltype(cc)::value;
+                        const float v = value(i, j, 4 * g + c, cs[c], bs[c]);
+                        if (live[i] && c < n_left0 - nc) store_elem(rowp[i], nc + c, wa.y_dtype, v);
+                    });
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+    }
+}
+
 template <int XDT, int WK>
 void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st)
 {
@@ -353,22 +493,38 @@ void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t
 // for uint4, the groups hold whole 32-element lane runs); the tiled kernel takes the rest.
 constexpr int64_t SKINNY_MAX_M = 64;
 
+template <int XDT, int WK>
+int launch_tiled(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                 const char *name)
+{
+    auto kern = gemm_wonly_tiled<XDT, WK>;
+    constexpr int lds = wt::lds_bytes<WK>();
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
+    static bool attr_set[64] = {};   // per device; the attribute is idempotent
+    if (dev < 64 && !attr_set[dev]) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+            return set_error(PSQ_E_DEVICE, "%s: cannot reserve %d bytes of LDS", name, lds);
+        attr_set[dev] = true;
+    }
+    const int64_t tiles = ((M + wt::BM - 1) / wt::BM) * ((N + wt::BN - 1) / wt::BN);
+    kern<<<dim3((unsigned)tiles), dim3(NTHREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    return check_launch(name);
+}
+
 template <int WK>
 int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa,
            hipStream_t st, const char *name)
 {
+    const uint16_t *xp = (const uint16_t *)x;
     if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (WK != W_UINT4 || wa.gs % 32 == 0)) {
-        if (x_dtype == PSQ_BF16) launch_skinny<PSQ_BF16, WK>((const uint16_t *)x, ldx, M, N, K, wa, st);
-        else launch_skinny<PSQ_F16, WK>((const uint16_t *)x, ldx, M, N, K, wa, st);
+        if (x_dtype == PSQ_BF16) launch_skinny<PSQ_BF16, WK>(xp, ldx, M, N, K, wa, st);
+        else launch_skinny<PSQ_F16, WK>(xp, ldx, M, N, K, wa, st);
         return check_launch(name);
     }
-    const int64_t nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    const dim3 grid((unsigned)nblk), block(NTHREADS);
-    if (x_dtype == PSQ_BF16)
-        gemm_wonly_kernel<PSQ_BF16, WK><<<grid, block, 0, st>>>((const uint16_t *)x, ldx, (int)M, (int)N, (int)K, wa);
-    else
-        gemm_wonly_kernel<PSQ_F16, WK><<<grid, block, 0, st>>>((const uint16_t *)x, ldx, (int)M, (int)N, (int)K, wa);
-    return check_launch(name);
+    if (ldx > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: ldx above 2^22", name);   // 32-bit row offsets
+    return x_dtype == PSQ_BF16 ? launch_tiled<PSQ_BF16, WK>(xp, ldx, M, N, K, wa, st, name)
+                               : launch_tiled<PSQ_F16, WK>(xp, ldx, M, N, K, wa, st, name);
 }
 
 int check_common(const char *name, const void *x, int x_dtype, int64_t ldx, const void *wq, const void *y, int y_dtype,
@@ -378,7 +534,7 @@ int check_common(const char *name, const void *x, int x_dtype, int64_t ldx, cons
     if (!x || !wq || !y) return set_error(PSQ_E_ARG, "%s: null pointer", name);
     if (x_dtype != PSQ_BF16 && x_dtype != PSQ_F16) return set_error(PSQ_E_ARG, "%s: activations must be bf16/f16", name);
     if (!valid_dtype(y_dtype) || (bias && !valid_dtype(bias_dtype))) return set_error(PSQ_E_ARG, "%s: bad dtype", name);
-    if (K == 0 || K % BK) return set_error(PSQ_E_SHAPE, "%s: K=%lld must be a positive multiple of %d", name, (long long)K, BK);
+    if (K == 0 || K % KSTAGE) return set_error(PSQ_E_SHAPE, "%s: K=%lld must be a positive multiple of %d", name, (long long)K, KSTAGE);
     if (ldx < K || ldx % 8 || ((uintptr_t)x & 15)) return set_error(PSQ_E_SHAPE, "%s: x rows must be 16-byte aligned", name);
     if (((uintptr_t)wq & 15)) return set_error(PSQ_E_SHAPE, "%s: weights must be 16-byte aligned", name);
     if (ldy < N) return set_error(PSQ_E_SHAPE, "%s: ldy < N", name);
@@ -399,8 +555,8 @@ int psq_gemm_w4a16(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq, c
     if (int e = check_common("gemm_w4a16", x, x_dtype, ldx, wq, y, y_dtype, ldy, bias, bias_dtype, M, N, K)) return e;
     if (M == 0 || N == 0) return PSQ_OK;
     if (!w_scale || !w_zero) return set_error(PSQ_E_ARG, "gemm_w4a16: null scale/zero");
-    if (group_size <= 0 || group_size % BK || K % group_size)
-        return set_error(PSQ_E_SHAPE, "gemm_w4a16: group size %d must be a multiple of %d dividing K", group_size, BK);
+    if (group_size <= 0 || group_size % KSTAGE || K % group_size)
+        return set_error(PSQ_E_SHAPE, "gemm_w4a16: group size %d must be a multiple of %d dividing K", group_size, KSTAGE);
     if (int e = require_device()) return e;
     WArgs wa{wq, w_scale, w_zero, nullptr, group_size, bias, bias_dtype, y, y_dtype, ldy};
     return launch<W_UINT4>(x, x_dtype, ldx, M, N, K, wa, (hipStream_t)stream, "gemm_w4a16");

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdarg.h>
+#include <utility>
+#include <type_traits>
 
 #include "../../../include/psquant.h"
 
@@ -228,6 +230,54 @@ __device__ __forceinline__ void tile_order(int pid, int nbm, int nbn, int group_
     const int r = lid - gid * in_group;
     pm = first_m + r % gsz;
     pn = r / gsz;
+}
+
+// ------------------------------------------------------------------ GEMM pipelines
+typedef __attribute__((address_space(3))) uint8_t *lds_ptr;
+typedef const __attribute__((address_space(1))) void *glb_ptr;
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4]<<14)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the K loop.  __syncthreads() carries a workgroup fence, which makes the
+// compiler drain every outstanding global->LDS load (vmcnt(0)) -- including the stages just put
+// in flight.  The loop instead waits explicitly for the stage it needs (wait_vmcnt) and for its
+// own LDS reads (lgkmcnt(0)), then meets the other waves; the asm memory clobber keeps the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void stage_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Reads an accumulator element through an AGPR operand.  The epilogue's arithmetic cannot take
+// AGPRs, and left to itself the register allocator then keeps the whole accumulator array in
+// VGPRs (and spills everything else); reading each element with an explicit AGPR-to-VGPR move
+// keeps the accumulators in the AGPR file for the MFMAs.
+__device__ __forceinline__ int agpr_read(int a)
+{
+    int v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+__device__ __forceinline__ int agpr_read(float a)
+{
+    int v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+
+// Calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1, expanded at compile time (an unroll
+// the optimizer cannot decline: register arrays indexed by I stay in registers).
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (f(std::integral_constant<int, I>{}), ...);
+    }(std::make_integer_sequence<int, N>{});
 }
 
 }  // namespace psq

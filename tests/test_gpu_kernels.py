@@ -257,7 +257,9 @@ def test_gemm_fp8(gpu, M, N, K, per_row):
 # M <= 64 with K % 128 == 0 runs the skinny (weight-streaming) kernel, the rest the tiled one
 @pytest.mark.parametrize("M,N,K,gs", [(512, 384, 1024, 128), (7, 256, 512, 64), (130, 100, 5120, 128),
                                       (64, 1000, 256, 256), (1, 2600, 5120, 128), (16, 513, 1024, 128),
-                                      (33, 64, 2048, 64), (65, 300, 1024, 128), (3, 100, 384, 64)])
+                                      (33, 64, 2048, 64), (65, 300, 1024, 128), (3, 100, 384, 64),
+                                      (600, 512, 2048, 256), (300, 768, 320, 64), (1, 256, 192, 64),
+                                      (257, 1280, 1024, 512)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
     from powershard_amd import ops
@@ -274,7 +276,7 @@ def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 512, 1024), (5, 40, 256), (200, 300, 5120), (1, 1030, 5120),
-                                   (48, 256, 1024), (64, 64, 640)])
+                                   (48, 256, 1024), (64, 64, 640), (700, 512, 640), (257, 1024, 192)])
 def test_gemm_w8a16(gpu, M, N, K):
     from powershard_amd import ops
     x = heavy_rows(M, K, seed=M, outlier_frac=0)
