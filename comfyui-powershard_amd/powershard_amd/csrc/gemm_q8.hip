@@ -8,41 +8,41 @@
 //
 // Tiling (MI355X-first): a persistent grid of one workgroup per CU walks 256 x 256 output tiles;
 // a workgroup is 4 waves, one per SIMD (2 x 2, each wave 128 x 128 = 4 x 4 MFMA tiles of 32 x 32,
-// accumulators in the AGPR half of the register file).  K runs in stages of 64 bytes through a
-// 4-deep LDS ring (4 x 32 KB) filled by direct global->LDS loads (global_load_lds_dwordx4: no
-// staging registers, no LDS write instructions), three stages in flight, continuously across the
-// tiles of a workgroup.  Fragments are double-buffered in registers so the LDS reads of the next
-// k-step overlap the MFMAs of the current one; one barrier per stage.  The epilogue converts the
-// accumulators in registers and stores them without an LDS round trip while the next tile's first
-// stages load.  MFMA-bound: 2 M N K ops per launch.
+// accumulators in the AGPR half of the register file).  K runs in stages of 128 bytes -- one full
+// cache line of every row -- through a 2-slot LDS ring (2 x 64 KB) filled by direct global->LDS
+// loads (global_load_lds_dwordx4: no staging registers, no LDS write instructions); a stage loads
+// while the previous one computes, continuously across the tiles of a workgroup.  Fragments are
+// double-buffered in registers so the LDS reads of the next k-step overlap the MFMAs of the
+// current one; one barrier per stage.  The epilogue converts the accumulators in registers and
+// stores them without an LDS round trip while the next tile's first stage loads.  MFMA-bound:
+// 2 M N K ops per launch.
 #include "psq_common.hpp"
 
 namespace psq {
 namespace {
 
-// Tuning knobs (compile-time): the int8 LDS swizzle and the tile grouping.
-#ifndef PSQ_Q8_SWZ
-#define PSQ_Q8_SWZ 1
-#endif
-#ifndef PSQ_Q8_SCHED
-#define PSQ_Q8_SCHED 1
-#endif
+// Tuning knobs (compile-time): the tile grouping and the positions of the int8 ring loads.
 #ifndef PSQ_Q8_GROUP_M
 #define PSQ_Q8_GROUP_M 8
 #endif
-
-constexpr int BM = 256, BN = 256, BK = 64;    // BK in bytes (= elements for int8/fp8)
-// LDS ring depth (NSTAGE - 1 stages in flight): 4 for int8; 3 for fp8, whose fragment sets
-// alternate per stage and so need an even number of stages between tile switches.
-#ifndef PSQ_Q8_RING_I8
-#define PSQ_Q8_RING_I8 4
+#ifndef PSQ_Q8_STAGED
+#define PSQ_Q8_STAGED 1
 #endif
-template <bool FP8> constexpr int ring_depth() { return FP8 ? 3 : PSQ_Q8_RING_I8; }
+#ifndef PSQ_Q8_DMA_I8
+#define PSQ_Q8_DMA_I8 1
+#endif
+#ifndef PSQ_Q8_DMA_F8
+#define PSQ_Q8_DMA_F8 0
+#endif
+
+constexpr int BM = 256, BN = 256, BK = 128;   // BK in bytes (= elements for int8/fp8)
+constexpr int NSTAGE = 2;                      // LDS ring slots: the stage computed, the stage loading
 constexpr int NTHREADS = 256;                  // 4 waves, one per SIMD
 constexpr int WAVE_M = 128, WAVE_N = 128;
 constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;   // 4 x 4 MFMA tiles of 32 x 32 per wave
-constexpr int STAGE_BYTES = BM * BK;                 // one operand, one stage (16 KB)
-constexpr int LOADS = (BM * BK / 1024) / (NTHREADS / 64);   // 1 KB wave loads per operand per stage (4)
+constexpr int STAGE_BYTES = BM * BK;                 // one operand, one stage (32 KB)
+constexpr int LOADS = (BM * BK / 1024) / (NTHREADS / 64);   // 1 KB wave loads per operand per stage (8)
+constexpr int LPS = 2 * LOADS;                       // ring loads per wave per stage (16)
 constexpr int GROUP_M = PSQ_Q8_GROUP_M;
 
 enum { OUT_BF16 = PSQ_BF16, OUT_F16 = PSQ_F16, OUT_F32 = PSQ_F32, OUT_I32 = 3 };
@@ -74,30 +74,48 @@ __device__ __forceinline__ void store1(void *p, int c, float v)
 }
 
 // LDS: the K-loop ring, then the epilogue operands.
-constexpr size_t kRingBytes = 4 * 2 * STAGE_BYTES;   // the deeper (int8) ring
+constexpr size_t kRingBytes = NSTAGE * 2 * STAGE_BYTES;
 
-// Stage rows are 64 bytes = four 16-byte chunks; a 32-lane MFMA fragment read touches 32
-// consecutive rows at one logical chunk.  int8 stores chunk ^ x(row) with x = (r1 ^ r3, r2) (bits
-// of the row): bijective in (r1, r2) and in (r2, r3), so both 8 consecutive rows (a 32-bank,
-// 128-byte LDS cycle) and 16 consecutive rows (a 64-bank, 256-byte cycle) hit distinct banks.
-// fp8 reads 32 bytes (two chunks) per lane, so it swaps whole 32-byte halves,
-// chunk ^ (((row >> 1) & 1) << 1), which keeps each lane's fragment contiguous and in k order.
-__device__ __forceinline__ int swz_i8(int r)
-{
-#if PSQ_Q8_SWZ == 0
-    return (r >> 1) & 3;
-#elif PSQ_Q8_SWZ == 1
-    return (((r >> 1) ^ (r >> 3)) & 1) | (r & 4) >> 1;
-#else
-    return (r >> 2) & 3;
-#endif
-}
+// Stage rows are 128 bytes = eight 16-byte chunks.  A fragment read touches 32 consecutive rows at
+// one logical chunk, 16 lanes (256 bytes, all 64 banks) per LDS cycle: bank group 8 (r & 1) +
+// physical chunk.  Chunk c of row r is stored at c ^ f(r), f(r) = (r ^ (r >> 3)) & 7, which is
+// bijective in row bits 0-2 (8 consecutive rows: distinct chunks) and, for a fixed bit 0, in bits
+// 1-3 (the 8 rows of one parity among 16 consecutive rows), so every read is conflict free.  fp8
+// reads two consecutive chunks per lane, each its own conflict-free read.
+__device__ __forceinline__ int chunk_xor(int row) { return (row ^ (row >> 3)) & 7; }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ chunk_xor(row)) << 4); }
 
+// Ring-load schedule: dma_slot(t, p) is the ring load (0-15: A blocks, then W blocks) issued
+// behind MFMA p (0-15) of k-step t, or -1.  Loads behind the last k-step (after the barrier) fill
+// the slot just freed with stage kt + 2 and are numbered first; loads behind the earlier k-steps
+// complete stage kt + 1 in the other slot before the barrier.  The fragment reads of the next
+// k-step go behind MFMAs 0-7.
 template <bool FP8>
-__device__ __forceinline__ int swz(int row, int chunk)
+constexpr int dma_slot(int t, int p)
 {
-    const int x = FP8 ? (((row >> 1) & 1) << 1) : swz_i8(row);
-    return row * BK + ((chunk ^ x) << 4);
+    if constexpr (!FP8) {
+        switch (PSQ_Q8_DMA_I8) {
+        case 0: return p >= 8 ? (t == 3 ? p - 8 : t == 0 ? p : -1) : -1;
+        case 1: return (p & 1) ? (t == 3 ? p >> 1 : t == 0 ? 8 + (p >> 1) : -1) : -1;
+        case 2:
+            if (t == 3) return (p >= 2 && p <= 12 && !(p & 1)) ? (p - 2) / 2 : -1;
+            if (t < 2) return (p % 3 == 1) ? 6 + 5 * t + p / 3 : -1;
+            return -1;
+        default: return (p & 3) == 1 ? 4 * ((t + 1) & 3) + (p >> 2) : -1;
+        }
+    } else {
+        switch (PSQ_Q8_DMA_F8) {
+        case 0: return t == 1 ? p : -1;
+        default: return t == 1 ? ((p & 1) ? p >> 1 : -1) : (p < 8 ? 8 + p : -1);
+        }
+    }
+}
+template <bool FP8>
+constexpr int late_loads()
+{
+    int n = 0;
+    for (int p = 0; p < 16; p++) n += dma_slot<FP8>(FP8 ? 1 : 3, p) >= 0;
+    return n;
 }
 
 template <bool FP8> struct Frag;
@@ -109,7 +127,10 @@ template <> struct Frag<true> { typedef v8i T; static constexpr int KSTEP = 64; 
 // used round-robin by consecutive tiles of a workgroup.
 constexpr int NSCALEBUF = 3;
 constexpr int SCALE_WORDS = BM + 2 * BN;
-constexpr size_t kSmemBytes = kRingBytes + NSCALEBUF * SCALE_WORDS * sizeof(float);
+// then, per wave, the staging buffer of the bf16 / f16 epilogue: 32 rows x 128 bytes
+constexpr int EPI_WAVE_BYTES = 32 * 128;
+constexpr size_t kEpiOffset = kRingBytes + NSCALEBUF * SCALE_WORDS * sizeof(float);
+constexpr size_t kSmemBytes = kEpiOffset + (NTHREADS / 64) * EPI_WAVE_BYTES;
 
 // Tiles of a persistent workgroup.  Hardware dispatches workgroup b to XCD b % 8; the tile
 // sequence (grouped raster order, GROUP_M row tiles per group) is cut into one contiguous chunk
@@ -158,10 +179,9 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];   // ring [NSTAGE][A | W], scales
     using Acc = typename std::conditional<FP8, v16f, v16i>::type;
     using FT = typename Frag<FP8>::T;
-    static_assert(BK / Frag<FP8>::KSTEP == (FP8 ? 1 : 2), "k-steps per stage: 2 for int8, 1 for fp8");
-    constexpr int LPS = 2 * LOADS;                 // ring DMA instructions per wave per stage
+    constexpr int KS = BK / Frag<FP8>::KSTEP;      // k-steps per stage: 4 (int8), 2 (fp8)
     constexpr bool SCALED = OUT != OUT_I32;
-    constexpr int NSTAGE = ring_depth<FP8>();
+    constexpr int LATE = late_loads<FP8>();         // loads of stage kt + 2 behind the last k-step
 
     // wave-uniform values in scalar registers: the LDS destination of every global->LDS load (M0)
     // is then computed without a VALU -> SGPR round trip
@@ -175,12 +195,11 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     uint32_t *const scale_lds = (uint32_t *)(smem + kRingBytes);
 
     // ---------------------------------------------------------------- ring loads
-    // global -> LDS: a wave load moves 1 KB = 16 rows x 4 chunks; lane L fills physical slot L of
-    // the block (row 16 b + L / 4, physical chunk L % 4) and reads the logical chunk stored there.
-    // The loads run NSTAGE - 1 stages ahead of the computation: during the last NSTAGE - 1 stages
-    // of a tile they fetch the first stages of the workgroup's next tile (pointer set `nx`); after
-    // its last tile a workgroup re-issues the tile's last stage, a load into a ring slot nobody
-    // reads again, so every stage issues the same number of loads and the waits are static.
+    // global -> LDS: a wave load moves 1 KB = 8 rows x 8 chunks (every row a full 128-byte cache
+    // line); lane L fills physical slot L of the block (row 8 b + L / 8, physical chunk L % 8) and
+    // reads the logical chunk stored there.  Stage s of a workgroup's sequence comes from its
+    // current tile while s < nk, then from its next tile (pointer set `n*`); past its last tile a
+    // workgroup re-loads the tile's last stage into the slot nobody reads any more.
     // A tile's rows are addressed as a wave-uniform base (A + m0 lda, W + n0 ldw: scalar
     // registers) plus a per-lane 32-bit offset -- the scalar-base form of global_load_lds, so a
     // load costs no 64-bit vector address arithmetic.  Rows past M (N) are clamped to the last
@@ -198,8 +217,8 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
 #pragma unroll
         for (int j = 0; j < LOADS; j++) {
             const int b = j * (NTHREADS / 64) + wave;
-            const int r = 16 * b + (lane >> 2);
-            const int c = (lane & 3) ^ (FP8 ? (((r >> 1) & 1) << 1) : swz_i8(r));
+            const int r = 8 * b + (lane >> 3);
+            const int c = (lane & 7) ^ chunk_xor(r);
             qa[j] = (uint32_t)(min(r, M - 1 - m0) * lda + c * 16);
             qw[j] = (uint32_t)(min(r, N - 1 - n0) * ldw + c * 16);
         }
@@ -216,6 +235,12 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             }
         }
     };
+    bool has_next = false;
+    // where stage s of the current tile's sequence comes from (see above)
+    auto source = [&](int s, bool &same, int64_t &koff) {
+        same = s < nk || !has_next;
+        koff = (int64_t)(s < nk ? s : (has_next ? s - nk : nk - 1)) * BK;
+    };
     // ring load q of a stage (q < LOADS: A block q, else W block q - LOADS), from the current tile
     // (same) or the next one, at byte offset koff along K, into ring slot `slot`.  The next tile's
     // lane offset is the current one plus a masked delta (a select between two offset arrays is
@@ -228,30 +253,25 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         const uint32_t off = q < LOADS ? oa[j] + (uint32_t)(doa[j] & mask) : ow[j] + (uint32_t)(dow[j] & mask);
         __builtin_amdgcn_global_load_lds((glb_ptr)(base + off), d, 16, 0, 0);
     };
-    auto issue_stage = [&](int slot, bool same, int64_t koff) {
-#pragma unroll
-        for (int q = 0; q < LPS; q++) issue_one(slot, same, koff, q);
-    };
 
     // MFMA operand layout (32 x 32 tiles): lane holds row (lane & 31) of W / of A and the k-slice
     // (lane >> 5) of the instruction's K; both operands use the same slice, so the dot products are
     // complete whatever order the hardware sums a slice in.
     const int frow = lane & 31, fk = lane >> 5;
-    // fragment q of a k-step: q < TM is A fragment q, else W fragment q - TM
+    // fragment q of k-step ks of the stage in `slot`: q < TM is A fragment q, else W fragment q - TM
     auto read_frag = [&](int slot, int ks, int q, FT (&fa)[TM], FT (&fw)[TN]) {
         const uint8_t *base = smem + slot * 2 * STAGE_BYTES + (q < TM ? 0 : STAGE_BYTES);
         const int r = (q < TM ? wm * WAVE_M + q * 32 : wn * WAVE_N + (q - TM) * 32) + frow;
         if constexpr (FP8) {
-            // two 16-byte reads: the compiler otherwise makes every 32-byte read wait for all
-            // global->LDS loads in flight (vmcnt(0)), whose completion the stage wait and barrier
-            // already order
-            const v4i lo = *(const v4i *)(base + swz<true>(r, 2 * fk));
-            const v4i hi = *(const v4i *)(base + swz<true>(r, 2 * fk) + 16);
+            // the lane's 32 bytes are chunks 4 ks + 2 fk and + 1: two 16-byte reads (a 32-byte
+            // read also makes the compiler wait for every global->LDS load in flight)
+            const v4i lo = *(const v4i *)(base + swz(r, 4 * ks + 2 * fk));
+            const v4i hi = *(const v4i *)(base + swz(r, 4 * ks + 2 * fk + 1));
             const v8i f = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             if (q < TM) fa[q] = f;
             else fw[q - TM] = f;
         } else {
-            const v4i f = *(const v4i *)(base + swz<false>(r, 2 * ks + fk));
+            const v4i f = *(const v4i *)(base + swz(r, 2 * ks + fk));
             if (q < TM) fa[q] = f;
             else fw[q - TM] = f;
         }
@@ -266,43 +286,6 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     };
     // Reads in the order the MFMAs (row-major over i, j) first need them: A0, W0..W3, A1..A3.
     constexpr int kReadOrder[TM + TN] = {0, 4, 5, 6, 7, 1, 2, 3};
-    // int8 half-stage schedules: behind MFMA q, fragment read kSchedRead[q] and ring load
-    // kSchedLoadA[q] (first half) / kSchedLoadB[q] (second half); -1 = none.  Global->LDS loads
-    // issued back to back stall the wave's MFMA issue, so they are spaced out; the reads go first.
-#if PSQ_Q8_SCHED == 0
-    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
-    constexpr int kSchedLoadA[16] = {-1, -1, -1, -1, -1, -1, -1, -1, 0, 1, 2, 3, 4, 5, 6, 7};
-    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
-#elif PSQ_Q8_SCHED == 1
-    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
-    constexpr int kSchedLoadA[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, 0, -1, 1, -1, 2, -1, 3};
-    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, 4, -1, 5, -1, 6, -1, 7};
-#elif PSQ_Q8_SCHED == 2
-    constexpr int kSchedRead[16] = {0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7, -1};
-    constexpr int kSchedLoadA[16] = {-1, 0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7};
-    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
-#elif PSQ_Q8_SCHED == 3
-    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
-    constexpr int kSchedLoadA[16] = {-1, -1, -1, 0, -1, -1, -1, 1, -1, -1, -1, 2, -1, -1, -1, 3};
-    constexpr int kSchedLoadB[16] = {-1, -1, -1, 4, -1, -1, -1, 5, -1, -1, -1, 6, -1, -1, -1, 7};
-#elif PSQ_Q8_SCHED == 4
-    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
-    constexpr int kSchedLoadA[16] = {-1, -1, -1, -1, -1, -1, -1, -1, 0, -1, 1, -1, 2, -1, 3, -1};
-    constexpr int kSchedLoadB[16] = {-1, -1, -1, -1, -1, -1, -1, -1, 4, -1, 5, -1, 6, -1, 7, -1};
-#elif PSQ_Q8_SCHED == 5
-    constexpr int kSchedRead[16] = {0, 1, 2, 3, 4, 5, 6, 7, -1, -1, -1, -1, -1, -1, -1, -1};
-    constexpr int kSchedLoadA[16] = {-1, 0, -1, -1, -1, 1, -1, -1, -1, 2, -1, -1, -1, 3, -1, -1};
-    constexpr int kSchedLoadB[16] = {-1, 4, -1, -1, -1, 5, -1, -1, -1, 6, -1, -1, -1, 7, -1, -1};
-#else
-    constexpr int kSchedRead[16] = {0, -1, 1, -1, 2, -1, 3, -1, 4, -1, 5, -1, 6, -1, 7, -1};
-    constexpr int kSchedLoadA[16] = {-1, -1, -1, 0, -1, -1, -1, 1, -1, -1, -1, 2, -1, -1, -1, 3};
-    constexpr int kSchedLoadB[16] = {-1, -1, -1, 4, -1, -1, -1, 5, -1, -1, -1, 6, -1, -1, -1, 7};
-#endif
-    constexpr int kLoadsB = [] {
-        int n = 0;
-        for (int q = 0; q < 16; q++) n += kSchedLoadB[q] >= 0;
-        return n;
-    }();
 
     // ---------------------------------------------------------------- epilogue
     // Lane (l & 31) owns output row m = m0 + 128 wm + 32 i + (l & 31); register 4 g + c of
@@ -348,6 +331,62 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             const float a = FP8 ? __int_as_float(x) : (float)x;
             return __builtin_fmaf(a, as[i] * w, b);
         };
+        if constexpr (PSQ_Q8_STAGED && (OUT == OUT_BF16 || OUT == OUT_F16)) {
+            if (ep.vec && n0 + BN <= N) {
+                // Full-width tile, aligned rows, 16-bit outputs: the wave's 128 x 128 block leaves
+                // in blocks of 32 rows x 64 columns through its private 4 KB LDS buffer (chunk
+                // swizzle as in the ring), so each store writes 8 rows x 128 bytes -- whole cache
+                // lines -- where a store straight from the registers writes 32 rows x 32 bytes.
+                // Within a block the lane pair (l, l + 32) first merges its column groups with one
+                // v_permlane32_swap per word (as in the direct path below).  LDS accesses of a
+                // wave execute in order, so the buffer needs no barrier.
+                uint8_t *const eb = smem + kEpiOffset + wave * EPI_WAVE_BYTES;
+                const int h = lane >> 5;
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int hj = 0; hj < 2; hj++) {
+#pragma unroll
+                        for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+                            for (int pr = 0; pr < 2; pr++) {
+                                const int j = 2 * hj + jj, nc = 32 * j + 16 * pr;
+                                float ws[2][4], bs[2][4];
+                                operands(nc, ws[0], bs[0]);
+                                operands(nc + 8, ws[1], bs[1]);
+                                uint32_t x[2], y[2];
+#pragma unroll
+                                for (int hh = 0; hh < 2; hh++) {
+                                    uint32_t *o = hh == 0 ? x : y;
+                                    const int r = 8 * pr + 4 * hh;
+                                    o[0] = pack2<OUT>(value(i, j, r, ws[hh][0], bs[hh][0]), value(i, j, r + 1, ws[hh][1], bs[hh][1]));
+                                    o[1] = pack2<OUT>(value(i, j, r + 2, ws[hh][2], bs[hh][2]), value(i, j, r + 3, ws[hh][3], bs[hh][3]));
+                                }
+                                uint32_t lo[2], hi[2];
+#pragma unroll
+                                for (int d = 0; d < 2; d++) {
+                                    const auto sw = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
+                                    lo[d] = sw[0];
+                                    hi[d] = sw[1];
+                                }
+                                // lane h now holds columns 32 jj + 16 pr + 8 h .. + 7 of the block
+                                const int ch = 4 * jj + 2 * pr + h;
+                                *(v4i *)(eb + frow * 128 + ((ch ^ chunk_xor(frow)) << 4)) =
+                                    v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                            }
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int row = 8 * q + (lane >> 3), ch = lane & 7;
+                            const v4i val = *(const v4i *)(eb + row * 128 + ((ch ^ chunk_xor(row)) << 4));
+                            const int m = m0 + wm * WAVE_M + 32 * i + row;
+                            if (m < M)
+                                *(v4i *)((uint8_t *)ep.y + ((int64_t)m * ep.ldy + n0 + wn * WAVE_N + 64 * hj + 8 * ch) * 2) = val;
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                return;
+            }
+        }
         if (ep.vec && n0 + BN <= N) {
             // Full-width tile, aligned rows.  Lanes l and l + 32 hold the same row: for column
             // groups g = 2p and 2p + 1 lane l has columns 16p + {0-3, 8-11} and lane l + 32 has
@@ -433,10 +472,23 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     };
 
     // ---------------------------------------------------------------- main loop
+    // Ring slot rs holds stage kt, slot rs ^ 1 stage kt + 1 (landed at the barrier before the last
+    // k-step of stage kt) and then stage kt + 2, whose loads start after that barrier: every wave
+    // has read its last fragments of stage kt by then.
+    // Prologue: stage 0 and (the A half of) stage 1 in flight, stage 0 landed, its first fragments.
     point_at(v, 0, ba, bw, oa, ow);
+    has_next = v + step < vend;
+    {
+        bool same;
+        int64_t koff;
+        source(0, same, koff);
 #pragma unroll
-    for (int s = 0; s < NSTAGE - 1; s++) issue_stage(s, true, (int64_t)min(s, nk - 1) * BK);
-    wait_vmcnt<(NSTAGE - 2) * LPS>();
+        for (int q = 0; q < LPS; q++) issue_one(0, same, koff, q);
+        source(1, same, koff);
+#pragma unroll
+        for (int q = 0; q < LATE; q++) issue_one(1, same, koff, q);
+    }
+    wait_vmcnt<LATE>();
     stage_barrier();
 
     FT fa0[TM], fw0[TN], fa1[TM], fw1[TN];
@@ -444,66 +496,55 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     int buf = 0;                     // epilogue-operand buffer of the tile being computed
 #pragma unroll
     for (int q = 0; q < TM + TN; q++) read_frag(0, 0, q, fa0, fw0);
-    // Stage kt loads stage kt + NSTAGE - 1: of this tile while that exists, else of the next
-    // tile (a K shorter than the lookahead gets one tile per workgroup, so it never gets there).
-    bool has_next = false;
-    // The instruction order inside a stage is fixed explicitly (sched_barrier after every step):
-    // with one wave per SIMD every issue slot not spent on an MFMA idles the matrix core, and the
-    // wave stalls wherever it waits for LDS reads still in flight.  So each half-stage first slots
-    // the fragment reads the next half-stage consumes behind its first MFMAs (they then have the
-    // rest of the half-stage to land), then the refill loads behind the following ones.
-    //   int8, one stage = two k-steps.  Half A: MFMAs of k-step 0 on (ca, cw); behind them the
-    //   reads of k-step 1 into (na, nw) and the refill of the ring slot read in the previous stage
-    //   (every wave passed the barrier that ended it).  Wait for the next stage, barrier.  Half B:
-    //   MFMAs of k-step 1 on (na, nw); behind them the next stage's k-step 0 reads into (ca, cw).
-    //   fp8, one k-step per stage.  Half A: MFMAs of rows 0-1 on (ca, cw) with the refill loads;
-    //   wait, barrier; half B: MFMAs of rows 2-3 with the next stage's reads into (na, nw).
-    auto stage = [&](int kt, FT (&ca)[TM], FT (&cw)[TN], FT (&na)[TM], FT (&nw)[TN]) {
-        const int t = kt + NSTAGE - 1;
-        const bool same = t < nk || !has_next;
-        const int64_t koff = (int64_t)(t < nk ? t : (has_next ? t - nk : nk - 1)) * BK;
-        const int slot = rs == 0 ? NSTAGE - 1 : rs - 1;
+
+    // One k-step: the 16 MFMAs of k-step t on (ca, cw); behind MFMAs 0-7 the fragment reads of
+    // the next k-step into (na, nw) (after the last k-step: k-step 0 of the next stage, from the
+    // other slot); the ring loads dma_slot places.
+    // The instruction order is fixed explicitly (sched_barrier after every MFMA): with one wave per
+    // SIMD every issue slot not spent on an MFMA idles the matrix core.
+    auto kstep = [&](auto tc, FT (&ca)[TM], FT (&cw)[TN], FT (&na)[TM], FT (&nw)[TN], bool s1, int64_t k1,
+                     bool s2, int64_t k2) {
+        constexpr int t = decltype(tc)::value;
+        constexpr bool last = t == KS - 1;
+        static_for<TM * TN>([&](auto pc) {
+            constexpr int p = decltype(pc)::value;
+            mfma(p / TN, p % TN, ca, cw);
+            if constexpr (p < TM + TN) read_frag(last ? rs ^ 1 : rs, last ? 0 : t + 1, kReadOrder[p], na, nw);
+            constexpr int d = dma_slot<FP8>(t, p);
+            if constexpr (d >= 0) {
+                if constexpr (last) issue_one(rs, s2, k2, d);
+                else issue_one(rs ^ 1, s1, k1, d);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    auto stage = [&](int kt) {
+        bool s1, s2;
+        int64_t k1, k2;
+        source(kt + 1, s1, k1);
+        source(kt + 2, s2, k2);
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
         if constexpr (!FP8) {
-#pragma unroll
-            for (int q = 0; q < TM * TN; q++) {
-                mfma(q / TN, q % TN, ca, cw);
-                if (kSchedRead[q] >= 0) read_frag(rs, 1, kReadOrder[kSchedRead[q]], na, nw);
-                if (kSchedLoadA[q] >= 0) issue_one(slot, same, koff, kSchedLoadA[q]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            wait_vmcnt<(NSTAGE - 2) * LPS - kLoadsB>();
+            kstep(I0{}, fa0, fw0, fa1, fw1, s1, k1, s2, k2);
+            kstep(I1{}, fa1, fw1, fa0, fw0, s1, k1, s2, k2);
+            kstep(std::integral_constant<int, 2>{}, fa0, fw0, fa1, fw1, s1, k1, s2, k2);
+            // stage kt + 1 landed for every wave; nobody reads stage kt's slot any more
+            wait_vmcnt<0>();
             stage_barrier();
-            rs = rs == NSTAGE - 1 ? 0 : rs + 1;
-#pragma unroll
-            for (int q = 0; q < TM * TN; q++) {
-                mfma(q / TN, q % TN, na, nw);
-                if (kSchedRead[q] >= 0) read_frag(rs, 0, kReadOrder[kSchedRead[q]], ca, cw);
-                if (kSchedLoadB[q] >= 0) issue_one(slot, same, koff, kSchedLoadB[q]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            kstep(std::integral_constant<int, 3>{}, fa1, fw1, fa0, fw0, s1, k1, s2, k2);
         } else {
-#pragma unroll
-            for (int q = 0; q < TM * TN / 2; q++) {
-                mfma(q / TN, q % TN, ca, cw);
-                issue_one(slot, same, koff, q);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            wait_vmcnt<(NSTAGE - 2) * LPS>();
+            kstep(I0{}, fa0, fw0, fa1, fw1, s1, k1, s2, k2);
+            wait_vmcnt<0>();
             stage_barrier();
-            rs = rs == NSTAGE - 1 ? 0 : rs + 1;
-#pragma unroll
-            for (int q = 0; q < TM * TN / 2; q++) {
-                mfma(TM / 2 + q / TN, q % TN, ca, cw);
-                read_frag(rs, 0, kReadOrder[q], na, nw);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            kstep(I1{}, fa1, fw1, fa0, fw0, s1, k1, s2, k2);
         }
+        rs ^= 1;
     };
 #pragma clang loop unroll(disable)
-    for (; v < vend; v += step) {
+    for (;;) {
         int m0, n0;
         tile_coords(v, nbm, nbn, m0, n0);
-        has_next = v + step < vend;
         if (has_next) {
             uint32_t qa[LOADS], qw[LOADS];
             point_at(v + step, buf == NSCALEBUF - 1 ? 0 : buf + 1, nba, nbw, qa, qw);
@@ -519,29 +560,20 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
-        if constexpr (!FP8) {
-            // int8 keeps fragment set 0 current at every stage boundary
 #pragma clang loop unroll(disable)
-            for (int kt = 0; kt < nk; kt++) stage(kt, fa0, fw0, fa1, fw1);
-        } else {
-            // fp8 swaps the sets per stage: pairs of stages (nk is even: K % 128 == 0)
-#pragma clang loop unroll(disable)
-            for (int kt = 0; kt < nk; kt += 2) {
-                stage(kt, fa0, fw0, fa1, fw1);
-                stage(kt + 1, fa1, fw1, fa0, fw0);
-            }
-        }
+        for (int kt = 0; kt < nk; kt++) stage(kt);
         epilogue(m0, n0, buf);
         buf = buf == NSCALEBUF - 1 ? 0 : buf + 1;
-        if (has_next) {
-            ba = nba;
-            bw = nbw;
+        if (!has_next) break;
+        ba = nba;
+        bw = nbw;
 #pragma unroll
-            for (int j = 0; j < LOADS; j++) {
-                oa[j] += (uint32_t)doa[j];
-                ow[j] += (uint32_t)dow[j];
-            }
+        for (int j = 0; j < LOADS; j++) {
+            oa[j] += (uint32_t)doa[j];
+            ow[j] += (uint32_t)dow[j];
         }
+        v += step;
+        has_next = v + step < vend;
     }
     // the re-issued loads past the last tile must land before the workgroup's LDS is released
     wait_vmcnt<0>();
@@ -577,7 +609,7 @@ int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int
     // persistent grid of one workgroup per CU; a K shorter than the ring's lookahead gets one
     // workgroup per tile (the kernel's loads then never cross into another tile)
     const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    const bool short_k = K / BK < ring_depth<FP8>() - 1;
+    const bool short_k = K / BK < NSTAGE;
     const int64_t grid = (short_k || tiles < cu_count(dev)) ? tiles : cu_count(dev);
     kern<<<dim3((unsigned)grid), dim3(NTHREADS), kSmemBytes, st>>>(a, lda, w, ldw, (int)M, (int)N, (int)K, ep);
     return check_launch(name);
