@@ -15,6 +15,10 @@
 namespace psq {
 namespace {
 
+#ifndef PSQ_W4_STREAM
+#define PSQ_W4_STREAM 1
+#endif
+
 constexpr int NTHREADS = 256;
 constexpr int KSTAGE = 64;                     // K granularity of every path
 
@@ -478,6 +482,249 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     }
 }
 
+// ------------------------------------------------------ uint4 streaming kernel (M <= 64)
+// The HBM-bound decode / prompt shapes of W4A16 with groups of a multiple of 128.  A workgroup
+// owns 64 or 128 weight rows (output columns, 16 per wave) over the whole K, so every weight byte
+// is read once and the activations once per workgroup; K runs in blocks of 128 (within one group).
+//  * Loads: per block, each wave's 16 rows x 64 bytes of nibbles, their group scales and zeros
+//    and a share of the activation block (16 MT rows x 256 bytes) go global->LDS into a
+//    (D + 1)-slot ring, D blocks ahead; one barrier per block.  Nothing is loaded into registers
+//    ahead of time, so the compiler's own load tracking adds no waits across the loop.
+//  * The lane dequantizes its 32 weights per block, w = round_16(fmaf(q, s, -z s)): one fma per
+//    weight where the other paths compute (q - z) * s, so a weight can differ from theirs by one
+//    16-bit ulp (when the two fp32 values straddle a rounding boundary, about 2^-16 of the
+//    weights) -- far inside the fp32-accumulation bar.  The VALU work per weight (nibble convert,
+//    fma, half a pack) is what bounds this kernel at small M.
+//  * MFMA 16x16x32 with the activations as the A operand: lane (n = l & 15, h = l >> 4) holds
+//    output column n (its weight row) and rows 4 h .. 4 h + 3 of each 16-row tile.  Lane group h
+//    carries k = 32 h + 8 t .. + 7 of the block in k-step t for both operands.
+namespace ws {
+// Per row-tile count MT: KH 128-k halves per block (BLK = 128 KH k) and 8 waves of 16 rows.  MT = 1
+// uses 256-k blocks: full 128-byte lines of every weight row per load and twice the bytes in flight
+// per ring slot, which the latency-bound decode shapes need; larger MT keep 128-k blocks so the
+// ring stays deep within the LDS.
+template <int MT> constexpr int KH() { return MT == 1 ? 2 : 1; }
+template <int MT> constexpr int BLK() { return 128 * KH<MT>(); }
+constexpr int ROWS = 128;                                   // weight rows per workgroup
+constexpr int NW = ROWS / 16;                               // waves
+template <int MT> constexpr int XSLOT() { return MT * 16 * BLK<MT>() * 2; }   // activations of a block
+template <int MT> constexpr int WSLOT() { return NW * 16 * BLK<MT>() / 2; }   // weights of a block
+constexpr int SZSLOT = NW * 256;                             // scale / zero words of a block
+template <int MT> constexpr int SLOT() { return XSLOT<MT>() + WSLOT<MT>() + SZSLOT; }
+#ifndef PSQ_W4S_DCAP
+#define PSQ_W4S_DCAP 64
+#endif
+template <int MT> constexpr int D() { return 163840 / SLOT<MT>() - 1 < PSQ_W4S_DCAP ? 163840 / SLOT<MT>() - 1 : PSQ_W4S_DCAP; }   // blocks in flight
+template <int MT> constexpr int lds_bytes() { return (D<MT>() + 1) * SLOT<MT>(); }
+}  // namespace ws
+
+template <int XDT, int MT>
+__global__ void __launch_bounds__(ws::NW * 64)
+gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
+{
+    using namespace ws;
+    constexpr int KHV = KH<MT>(), B = BLK<MT>(), DD = D<MT>(), NX = DD + 1;
+    constexpr int XS = XSLOT<MT>(), WS = WSLOT<MT>(), SL = SLOT<MT>();
+    static_assert(DD >= 2, "ring too shallow");
+    using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nr = lane & 15, h = lane >> 4;
+    const int nb = K / B;
+    const int G = K / wa.gs;                                 // groups per row
+    const int64_t wld = K / 2;
+    const int row0 = blockIdx.x * ROWS + 16 * wave;         // the wave's first weight row
+
+    // ---- ring loads of a block (all global->LDS; rows past N clamp to the last row)
+    // weights: the wave's 16 rows x 64 KH bytes in KH loads of 1 KB; lane L of load d fills row
+    // (16 / KH) d + L / (4 KH), physical chunk L % (4 KH), holding logical chunk pc ^ f(row),
+    // f(n) = (n >> (3 - KH)) & (4 KH - 1), so the 16 lanes reading one chunk of 16 rows hit 16
+    // distinct bank groups
+    uint32_t wo[KHV];
+#pragma unroll
+    for (int d = 0; d < KHV; d++) {
+        const int r = (16 / KHV) * d + lane / (4 * KHV), pc = lane % (4 * KHV);
+        const int c = pc ^ ((r >> (3 - KHV)) & (4 * KHV - 1));
+        wo[d] = (uint32_t)(min(row0 + r, N - 1) * wld + c * 16);
+    }
+    // scales and zeros: lane L fetches, for array L >> 5 (scale, zero), row (L >> (KH - 1)) & 15
+    // and 128-k half L & (KH - 1), one 16-bit value into its 32-bit slot.  The group of half j of
+    // block b is (KH b + j) / hg (hg = gs / 128 halves per group), kept as a running quotient and
+    // remainder of KH b on the scalar unit (no per-lane division).
+    const bool szhi = (lane & (KHV - 1)) != 0;
+    const uint16_t *const szrow = (lane < 32 ? wa.scale16 : wa.zero16) +
+                                  (int64_t)min(row0 + ((lane >> (KHV - 1)) & 15), N - 1) * G;
+    const int hg = wa.gs / 128;
+    int gq = 0, gr = 0;                                      // KH b = gq hg + gr for the next block issued
+    // activations: 1 KB = (4 / KH) rows x 256 KH bytes; lane L fills row (4 / KH) d + L / (16 KH),
+    // physical chunk L % (16 KH), holding logical chunk pc ^ (row & 15).  Only the row groups
+    // holding rows below M are loaded (rows past M feed output rows that are never stored); wave w
+    // loads groups w, w + NW, ..: xd of them, a wave-uniform count that picks its vmcnt waits.
+    constexpr int RPL = 4 / KHV;                             // activation rows per load
+    constexpr int XDMAX = (16 * MT / RPL + NW - 1) / NW;
+    static_assert(XDMAX <= 2, "at most two activation loads per wave and block");
+    const int nxl = (M + RPL - 1) / RPL;
+    const int xd = wave < nxl ? min(XDMAX, (nxl - wave + NW - 1) / NW) : 0;
+    uint32_t xo[XDMAX];
+#pragma unroll
+    for (int i = 0; i < XDMAX; i++) {
+        const int row = RPL * (wave + NW * i) + lane / (16 * KHV), pc = lane % (16 * KHV);
+        xo[i] = (uint32_t)(min(row, M - 1) * ldx * 2 + (pc ^ (row & 15)) * 16);
+    }
+    // blocks are issued in order, once each (past the end: the last block again)
+    auto issue = [&](int b, int slot) {
+        const int bc = min(b, nb - 1);
+        uint8_t *const sl = smem + slot * SL;
+        const uint8_t *const wb = wa.wq + (int64_t)bc * (B / 2);
+#pragma unroll
+        for (int d = 0; d < KHV; d++)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(wb + wo[d]), (lds_ptr)(sl + XS + (WS / NW) * wave + 1024 * d), 16,
+                                             0, 0);
+        const int g0 = min(gq, G - 1), g1 = min(gq + (gr + 1 >= hg ? 1 : 0), G - 1);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(szrow + (szhi ? g1 : g0)), (lds_ptr)(sl + XS + WS + 256 * wave), 2,
+                                         0, 0);
+        gr += KHV;
+        if (gr >= hg) { gr -= hg; gq++; }
+        if (gr >= hg) { gr -= hg; gq++; }
+#pragma unroll
+        for (int i = 0; i < XDMAX; i++)
+            if (i < xd)
+                __builtin_amdgcn_global_load_lds((glb_ptr)((const uint8_t *)x + (int64_t)bc * B * 2 + xo[i]),
+                                                 (lds_ptr)(sl + 1024 * (wave + NW * i)), 16, 0, 0);
+    };
+
+    // block b's operands in registers: activation fragments, packed weights, scale and -z s.
+    // Lane group h carries k = 32 KH h + 8 s .. + 7 of the block in k-step s (0 .. 4 KH - 1).
+    struct Ops { XV xf[MT][4 * KHV]; v4i wv[KHV]; float sc, zs; };
+    auto read = [&](int slot, Ops &o) {
+        const uint8_t *const sl = smem + slot * SL;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int t = 0; t < 4 * KHV; t++) {
+                const int row = 16 * mt + nr, c = 4 * KHV * h + t;
+                o.xf[mt][t] = __builtin_bit_cast(XV, *(const v4i *)(sl + row * (B * 2) + ((c ^ (row & 15)) << 4)));
+            }
+#pragma unroll
+        for (int i = 0; i < KHV; i++) {
+            const int c = KHV * h + i;
+            o.wv[i] = *(const v4i *)(sl + XS + (WS / NW) * wave + nr * (B / 2) +
+                                     ((c ^ ((nr >> (3 - KHV)) & (4 * KHV - 1))) << 4));
+        }
+        const int si = (nr << (KHV - 1)) | ((KHV * h) >> 2);
+        const uint32_t *sz = (const uint32_t *)(sl + XS + WS + 256 * wave);
+        o.sc = f16_to_f32(sz[si]);
+        o.zs = -(f16_to_f32(sz[32 + si]) * o.sc);
+    };
+    // w = round_16(fmaf(q, s, -z s)), then the block's MFMAs
+    v4f acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](const Ops &o) {
+        // all the block's weight fragments first: the MFMAs then read registers no VALU op still
+        // writes (a fragment register rewritten behind its MFMA costs a wait per k-step)
+        XV wfs[4 * KHV];
+#pragma unroll
+        for (int t = 0; t < 4 * KHV; t++) {
+            const uint32_t p = (uint32_t)o.wv[t >> 2][t & 3];
+            const uint32_t lo = p & 0x0f0f0f0fu, hi = (p >> 4) & 0x0f0f0f0fu;   // even / odd k
+            float q0[4], q1[4];
+            ubytes_to_f32(lo, q0);
+            ubytes_to_f32(hi, q1);
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = pack2<XDT>(__builtin_fmaf(q0[e], o.sc, o.zs), __builtin_fmaf(q1[e], o.sc, o.zs));
+            wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+        }
+#pragma unroll
+        for (int t = 0; t < 4 * KHV; t++) {
+            const XV &wf = wfs[t];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                if constexpr (XDT == PSQ_BF16)
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.xf[mt][t], wf, acc[mt], 0, 0, 0);
+                else
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.xf[mt][t], wf, acc[mt], 0, 0, 0);
+            }
+        }
+    };
+    // a block landed for every wave (own loads per block: KH + 1 + xd; `younger` blocks after it)
+    auto wait_block = [&](auto youngerc) {
+        constexpr int younger = decltype(youngerc)::value, L = KHV + 1;
+        if (xd == 0) wait_vmcnt<younger * L>();
+        else if (XDMAX == 1 || xd == 1) wait_vmcnt<younger * (L + 1)>();
+        else wait_vmcnt<younger * (L + 2)>();
+        stage_barrier();
+    };
+
+    // Software pipeline: the LDS reads of block b + 1 are issued before block b's dequantization
+    // and MFMAs, which cover their latency.  Block b's slot is refilled once every wave has passed
+    // the barrier of block b + 1 (it read block b before that).
+#pragma unroll
+    for (int b = 0; b < DD; b++) issue(b, b);
+    Ops oa, ob;
+    wait_block(std::integral_constant<int, DD - 1>{});
+    read(0, oa);
+    int rslot = 1, fslot = DD;                               // slot of block b + 1, slot to refill
+    auto step = [&](int b, const Ops &cur, Ops &nxt) {
+        if (b + 1 < nb) {
+            wait_block(std::integral_constant<int, DD - 2>{});
+            read(rslot, nxt);
+            rslot = rslot == NX - 1 ? 0 : rslot + 1;
+        }
+        issue(b + DD, fslot);
+        fslot = fslot == NX - 1 ? 0 : fslot + 1;
+        compute(cur);
+    };
+    for (int b = 0; b < nb; b += 2) {
+        step(b, oa, ob);
+        if (b + 1 < nb) step(b + 1, ob, oa);
+    }
+    wait_vmcnt<0>();
+    // y[m][n] = round_out(acc + bias[n]); lane: n = its row, m = 16 mt + 4 h + v
+    const int n = row0 + nr;
+    if (n < N) {
+        const float bb = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = 16 * mt + 4 * h + v;
+                if (m < M) store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype, acc[mt][v] + bb);
+            }
+    }
+}
+
+template <int XDT, int MT>
+int launch_stream_mt(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                     const char *name)
+{
+    auto kern = gemm_w4_stream<XDT, MT>;
+    constexpr int lds = ws::lds_bytes<MT>();
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
+    static bool attr_set[64] = {};
+    if (dev < 64 && !attr_set[dev]) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+            return set_error(PSQ_E_DEVICE, "%s: cannot reserve %d bytes of LDS", name, lds);
+        attr_set[dev] = true;
+    }
+    const dim3 grid((unsigned)((N + ws::ROWS - 1) / ws::ROWS)), block(ws::NW * 64);
+    kern<<<grid, block, lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    return check_launch(name);
+}
+
+template <int XDT>
+int launch_stream(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                  const char *name)
+{
+    const int mt = (int)((M + 15) / 16);
+    if (mt == 1) return launch_stream_mt<XDT, 1>(x, ldx, M, N, K, wa, st, name);
+    if (mt == 2) return launch_stream_mt<XDT, 2>(x, ldx, M, N, K, wa, st, name);
+    if (mt == 3) return launch_stream_mt<XDT, 3>(x, ldx, M, N, K, wa, st, name);
+    return launch_stream_mt<XDT, 4>(x, ldx, M, N, K, wa, st, name);
+}
+
 template <int XDT, int WK>
 void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st)
 {
@@ -517,6 +764,11 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
            hipStream_t st, const char *name)
 {
     const uint16_t *xp = (const uint16_t *)x;
+    if (WK == W_UINT4 && PSQ_W4_STREAM && M <= SKINNY_MAX_M && wa.gs % 128 == 0 &&
+        K % (M <= 16 ? ws::BLK<1>() : ws::BLK<2>()) == 0 && ldx <= (1LL << 22)) {
+        return x_dtype == PSQ_BF16 ? launch_stream<PSQ_BF16>(xp, ldx, M, N, K, wa, st, name)
+                                   : launch_stream<PSQ_F16>(xp, ldx, M, N, K, wa, st, name);
+    }
     if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (WK != W_UINT4 || wa.gs % 32 == 0)) {
         if (x_dtype == PSQ_BF16) launch_skinny<PSQ_BF16, WK>(xp, ldx, M, N, K, wa, st);
         else launch_skinny<PSQ_F16, WK>(xp, ldx, M, N, K, wa, st);
