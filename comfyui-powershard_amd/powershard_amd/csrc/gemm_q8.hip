@@ -28,6 +28,12 @@ namespace {
 #ifndef PSQ_Q8_STAGED
 #define PSQ_Q8_STAGED 1
 #endif
+#ifndef PSQ_Q8_NT
+#define PSQ_Q8_NT 1
+#endif
+#ifndef PSQ_Q8_HOIST
+#define PSQ_Q8_HOIST 1
+#endif
 #ifndef PSQ_Q8_DMA_I8
 #define PSQ_Q8_DMA_I8 1
 #endif
@@ -342,18 +348,41 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                 // wave execute in order, so the buffer needs no barrier.
                 uint8_t *const eb = smem + kEpiOffset + wave * EPI_WAVE_BYTES;
                 const int h = lane >> 5;
+                constexpr bool HOIST = PSQ_Q8_HOIST && !FP8;
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+                for (int hj = 0; hj < 2; hj++) {
+                    // with HOIST the half's column operands are read once for all four row blocks
+                    float hws[HOIST ? 2 : 1][HOIST ? 2 : 1][2][4], hbs[HOIST ? 2 : 1][HOIST ? 2 : 1][2][4];
+                    if constexpr (HOIST) {
 #pragma unroll
-                    for (int hj = 0; hj < 2; hj++) {
+                        for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+                            for (int pr = 0; pr < 2; pr++) {
+                                const int nc = 32 * (2 * hj + jj) + 16 * pr;
+                                operands(nc, hws[jj][pr][0], hbs[jj][pr][0]);
+                                operands(nc + 8, hws[jj][pr][1], hbs[jj][pr][1]);
+                            }
+                    }
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
 #pragma unroll
                         for (int jj = 0; jj < 2; jj++)
 #pragma unroll
                             for (int pr = 0; pr < 2; pr++) {
                                 const int j = 2 * hj + jj, nc = 32 * j + 16 * pr;
                                 float ws[2][4], bs[2][4];
-                                operands(nc, ws[0], bs[0]);
-                                operands(nc + 8, ws[1], bs[1]);
+                                if constexpr (HOIST) {
+#pragma unroll
+                                    for (int u = 0; u < 2; u++)
+#pragma unroll
+                                        for (int c = 0; c < 4; c++) {
+                                            ws[u][c] = hws[jj][pr][u][c];
+                                            bs[u][c] = hbs[jj][pr][u][c];
+                                        }
+                                } else {
+                                    operands(nc, ws[0], bs[0]);
+                                    operands(nc + 8, ws[1], bs[1]);
+                                }
                                 uint32_t x[2], y[2];
 #pragma unroll
                                 for (int hh = 0; hh < 2; hh++) {
@@ -379,11 +408,15 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                             const int row = 8 * q + (lane >> 3), ch = lane & 7;
                             const v4i val = *(const v4i *)(eb + row * 128 + ((ch ^ chunk_xor(row)) << 4));
                             const int m = m0 + wm * WAVE_M + 32 * i + row;
-                            if (m < M)
-                                *(v4i *)((uint8_t *)ep.y + ((int64_t)m * ep.ldy + n0 + wn * WAVE_N + 64 * hj + 8 * ch) * 2) = val;
+                            if (m < M) {
+                                v4i *dst = (v4i *)((uint8_t *)ep.y + ((int64_t)m * ep.ldy + n0 + wn * WAVE_N + 64 * hj + 8 * ch) * 2);
+                                if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val, dst);
+                                else *dst = val;
+                            }
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     }
+                }
                 return;
             }
         }
