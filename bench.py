@@ -328,6 +328,24 @@ def extra_w8a16(args):
     res = dict(workload="int8 weight-only (W8A16) 1024x5120x5120", kernel_ms=per["gemm_w8a16"],
                tflops=flops / (per["gemm_w8a16"] * 1e-3) / 1e12)
     log(f"[bench] w8a16: {per['gemm_w8a16'] * 1e3:.1f} us, {res['tflops']:.0f} TFLOP/s")
+    # Int8Linear (powershard/operations.py:96-132) with ConvRot storage on the same shape: the kernel
+    # path (rotate + W8A16) against the reference's 256-row tile dequantization + F.linear
+    from powershard_amd.operations import Int8Linear
+    layers = []
+    for native in (True, False):
+        lin = Int8Linear(torch.nn.Linear(K, N, bias=True), dict(convrot=True, group_size=256), rows=256)
+        lin = lin.to_empty(device="cuda")
+        lin.weight.data.copy_(q)
+        lin.weight_scale.data.copy_(s.reshape(-1, 1))
+        lin.bias = torch.nn.Parameter(b.half(), requires_grad=False)
+        lin._ps_native = native
+        layers.append(lin)
+    xh = x.half()
+    for name, lin in zip(("int8linear_kernel_ms", "int8linear_tiles_ms"), layers):
+        res[name] = untimed_kernel_ms(lambda: lin(xh), max(args.steps, 20), args.warmup)
+    res["int8linear_workload"] = "Int8Linear ConvRot g=256, fp16, 1024x5120x5120: rotate + W8A16 vs 256-row tiles"
+    log(f"[bench] Int8Linear: kernels {res['int8linear_kernel_ms'] * 1e3:.1f} us, "
+        f"tile dequant {res['int8linear_tiles_ms'] * 1e3:.1f} us")
     return res
 
 

@@ -26,6 +26,7 @@ SIGNATURES = {
     "psq_device_supported": (_I, [_I]),
     "psq_quantize_rows_i8": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P, _I64, _P, _P]),
     "psq_quantize_rows_fp8": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P, _I64, _P, _P]),
+    "psq_rotate_rows": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _I, _I64, _P]),
     "psq_gemm_i8": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_i8_i32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_fp8": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),

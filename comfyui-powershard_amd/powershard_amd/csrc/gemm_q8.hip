@@ -107,7 +107,8 @@ constexpr int dma_slot(int t, int p)
             if (t == 3) return (p >= 2 && p <= 12 && !(p & 1)) ? (p - 2) / 2 : -1;
             if (t < 2) return (p % 3 == 1) ? 6 + 5 * t + p / 3 : -1;
             return -1;
-        default: return (p & 3) == 1 ? 4 * ((t + 1) & 3) + (p >> 2) : -1;
+        case 3: return (p & 3) == 1 ? 4 * ((t + 1) & 3) + (p >> 2) : -1;
+        default: return t == 3 ? ((p & 1) ? (p >> 1) : 8 + (p >> 1)) : -1;
         }
     } else {
         switch (PSQ_Q8_DMA_F8) {

@@ -182,6 +182,68 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
     }
 }
 
+// Rotation only: y = round_out(2^-k T(x)) per group (x H with H the normalized regular Hadamard),
+// the activation side of a ConvRot weight-only linear, x W^T = (x H)(q s)^T for weights stored as
+// W H.  Same thread layout and transform as the quantizer; no reduction, so no barrier.
+template <int DT, int ROTK, int OUT, int P>
+__global__ void __launch_bounds__(kMaxThreads)
+rotate_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int K, void *__restrict__ y, int64_t ldy)
+{
+    const int t = threadIdx.x, T = blockDim.x, row = blockIdx.x;
+    const float post = ROTK ? __builtin_ldexpf(1.0f, -ROTK) : 1.0f;
+    const uint16_t *src = x + (int64_t)row * ldx + (int64_t)t * kElemsPerThread;
+#pragma unroll
+    for (int c = 0; c < P; c++) {
+        if ((c * T + t) * kElemsPerThread >= K) break;
+        const int64_t off = (int64_t)c * T * kElemsPerThread;
+        v4i raw[2] = {*(const v4i *)(src + off), *(const v4i *)(src + off + 8)};
+        float v[16];
+        to_f32<DT>(raw, v);
+        rotate16<ROTK>(v);
+        const int64_t e0 = (int64_t)row * ldy + (int64_t)(c * T + t) * kElemsPerThread;
+        if constexpr (OUT == PSQ_F32) {
+            float *o = (float *)y + e0;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                *(v4f *)(o + 4 * i) = v4f{v[4 * i] * post, v[4 * i + 1] * post, v[4 * i + 2] * post, v[4 * i + 3] * post};
+        } else {
+            uint32_t w[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) w[i] = pack_half2<OUT>(v[2 * i] * post, v[2 * i + 1] * post);
+            uint16_t *o = (uint16_t *)y + e0;
+            *(v4i *)o = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            *(v4i *)(o + 8) = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+        }
+    }
+}
+
+template <int DT, int OUT, int P>
+int launch_rotate_p(const uint16_t *xp, int64_t M, int64_t K, int64_t ldx, int rotk, int threads, void *y,
+                    int64_t ldy, hipStream_t st)
+{
+    const dim3 grid((unsigned)M), block(threads);
+    switch (rotk) {
+#define PSQ_CASE(RK)                                                                                    \
+    case RK: rotate_rows_kernel<DT, RK, OUT, P><<<grid, block, 0, st>>>(xp, ldx, (int)K, y, ldy); break;
+        PSQ_CASE(0) PSQ_CASE(1) PSQ_CASE(2) PSQ_CASE(3) PSQ_CASE(4) PSQ_CASE(5)
+#undef PSQ_CASE
+    default:
+        return set_error(PSQ_E_SHAPE, "rotation group 4^%d unsupported", rotk);
+    }
+    return check_launch("rotate_rows");
+}
+
+template <int DT, int OUT>
+int launch_rotate(const void *x, int64_t M, int64_t K, int64_t ldx, int rotk, void *y, int64_t ldy, hipStream_t st)
+{
+    const int64_t chunks16 = K / kElemsPerThread;
+    const int P = chunks16 <= kMaxThreads ? 1 : 2;
+    const int threads = (int)((chunks16 + P - 1) / P + 63) / 64 * 64;
+    const uint16_t *xp = (const uint16_t *)x;
+    if (P == 2) return launch_rotate_p<DT, OUT, 2>(xp, M, K, ldx, rotk, threads, y, ldy, st);
+    return launch_rotate_p<DT, OUT, 1>(xp, M, K, ldx, rotk, threads, y, ldy, st);
+}
+
 template <int DT, bool FP8, int P, int R>
 int launch_quant_p(const uint16_t *xp, int64_t M, int64_t K, int64_t ldx, int rotk, int threads,
                    const float *static_scale, uint8_t *q, int64_t ldq, float *scale, hipStream_t st)
@@ -215,6 +277,48 @@ int launch_quant(const void *x, int64_t M, int64_t K, int64_t ldx, int rotk,
     return launch_quant_p<DT, FP8, 1, 1>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st);
 }
 
+// rot_group 0 (rotk 0) or a power of 4 in [4, 1024] dividing K (rotk = its base-4 log)
+int rot_log4(int rot_group, int64_t K, int &rotk)
+{
+    rotk = 0;
+    if (!rot_group) return PSQ_OK;
+    int g = rot_group;
+    while (g > 1 && (g & 3) == 0) { g >>= 2; rotk++; }
+    if (g != 1 || rotk < 1 || rotk > 5 || K % rot_group)
+        return set_error(PSQ_E_SHAPE, "rotation group %d must be a power of 4 in [4,1024] dividing K=%lld", rot_group,
+                         (long long)K);
+    return PSQ_OK;
+}
+
+int rotate_rows(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int rot_group, void *y, int y_dtype,
+                int64_t ldy, void *stream)
+{
+    if (M < 0 || K < 0) return set_error(PSQ_E_ARG, "negative size M=%lld K=%lld", (long long)M, (long long)K);
+    if (M == 0) return PSQ_OK;
+    if (!x || !y) return set_error(PSQ_E_ARG, "null pointer");
+    if (x_dtype != PSQ_BF16 && x_dtype != PSQ_F16)
+        return set_error(PSQ_E_ARG, "activations must be bf16 or f16 (dtype %d)", x_dtype);
+    if (!valid_dtype(y_dtype)) return set_error(PSQ_E_ARG, "bad output dtype %d", y_dtype);
+    if (K == 0 || K % kElemsPerThread || K > kMaxK)
+        return set_error(PSQ_E_SHAPE, "K=%lld must be a positive multiple of 16 and <= %d", (long long)K, kMaxK);
+    if (ldx < K || ldy < K || ldx % 8 || ldy % 8)
+        return set_error(PSQ_E_SHAPE, "strides ldx=%lld ldy=%lld must be multiples of 8 covering K=%lld",
+                         (long long)ldx, (long long)ldy, (long long)K);
+    if (((uintptr_t)x & 15) || ((uintptr_t)y & 15)) return set_error(PSQ_E_SHAPE, "x and y must be 16-byte aligned");
+    if (M > 0x7fffffffLL) return set_error(PSQ_E_SHAPE, "M=%lld too large", (long long)M);
+    int rotk = 0;
+    if (int e = rot_log4(rot_group, K, rotk)) return e;
+    if (int e = require_device()) return e;
+    hipStream_t st = (hipStream_t)stream;
+    auto go = [&](auto dtc) {
+        constexpr int DT = decltype(dtc)::value;
+        if (y_dtype == PSQ_BF16) return launch_rotate<DT, PSQ_BF16>(x, M, K, ldx, rotk, y, ldy, st);
+        if (y_dtype == PSQ_F16) return launch_rotate<DT, PSQ_F16>(x, M, K, ldx, rotk, y, ldy, st);
+        return launch_rotate<DT, PSQ_F32>(x, M, K, ldx, rotk, y, ldy, st);
+    };
+    return x_dtype == PSQ_BF16 ? go(std::integral_constant<int, PSQ_BF16>{}) : go(std::integral_constant<int, PSQ_F16>{});
+}
+
 int quantize_rows(bool fp8, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   int rot_group, const float *static_scale, uint8_t *q, int64_t ldq, float *scale,
                   void *stream)
@@ -233,13 +337,7 @@ int quantize_rows(bool fp8, const void *x, int x_dtype, int64_t M, int64_t K, in
         return set_error(PSQ_E_SHAPE, "x and q must be 16-byte aligned");
     if (M > 0x7fffffffLL) return set_error(PSQ_E_SHAPE, "M=%lld too large", (long long)M);
     int rotk = 0;
-    if (rot_group) {
-        int g = rot_group;
-        while (g > 1 && (g & 3) == 0) { g >>= 2; rotk++; }
-        if (g != 1 || rotk < 1 || rotk > 5 || K % rot_group)
-            return set_error(PSQ_E_SHAPE, "rotation group %d must be a power of 4 in [4,1024] dividing K=%lld",
-                             rot_group, (long long)K);
-    }
+    if (int e = rot_log4(rot_group, K, rotk)) return e;
     if (int e = require_device()) return e;
     hipStream_t st = (hipStream_t)stream;
     if (fp8)
@@ -265,6 +363,12 @@ int psq_quantize_rows_fp8(const void *x, int x_dtype, int64_t M, int64_t K, int6
                           const float *static_scale, uint8_t *q, int64_t ldq, float *scale, void *stream)
 {
     return psq::quantize_rows(true, x, x_dtype, M, K, ldx, rot_group, static_scale, q, ldq, scale, stream);
+}
+
+int psq_rotate_rows(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int rot_group, void *y,
+                    int y_dtype, int64_t ldy, void *stream)
+{
+    return psq::rotate_rows(x, x_dtype, M, K, ldx, rot_group, y, y_dtype, ldy, stream);
 }
 
 }  // extern "C"

@@ -1,9 +1,15 @@
-"""ConvRot int8 helpers and the row-tiled Int8Linear (the ``precision=int8_fp16`` storage).
+"""ConvRot int8 helpers and Int8Linear (the ``precision=int8_fp16`` storage).
 
 Mirrors powershard/operations.py:72-155: ``regular_hadamard`` (72-81), ``dequantize_rows``
 (84-93), ``Int8Linear`` (96-132) and ``install_int8`` (135-155).  On a GPU the row dequantization
 runs the gfx950 kernel (``psq_dequant_i8_rows``: q * s, then the ConvRot inverse by the fast
 transform); on the CPU it is the reference's torch formula.
+
+On a gfx950 GPU Int8Linear does not dequantize at all: since the stored weight is W H per ConvRot
+group (H symmetric, H H^T = I), x W^T = (x H)(q s)^T, so the forward is the activation rotation
+(``psq_rotate_rows``) and the int8 weight-only GEMM (``psq_gemm_w8a16``, q exact in fp16, s in the
+epilogue).  The reference's per-tile dequantize + F.linear remains the path on the CPU, in the fp32
+island and for shapes the kernels do not take.
 """
 from functools import lru_cache
 
@@ -55,19 +61,49 @@ class Int8Linear(nn.Module):
         safe = getattr(self, "_ps_safe", False)
         tracker = getattr(self, "_ps_tracker", None)
         x = x.float() if safe else x.half()
-        out = torch.empty(x.shape[:-1] + (self.out_features,), dtype=x.dtype, device=x.device)
-        for a in range(0, self.out_features, self.rows):
-            b = min(a + self.rows, self.out_features)
-            w = dequantize_rows(self.weight[a:b], self.weight_scale[a:b], self.convrot, self.group_size,
-                                dtype=torch.float32 if safe else torch.float16, check=tracker is None)
-            bias = None if self.bias is None else self.bias[a:b].to(x.dtype)
-            out[..., a:b] = F.linear(x, w, bias)
-            del w
+        out = None
+        if not safe and x.device.type == "cuda" and getattr(self, "_ps_native", True):
+            out = self._native_forward(x, check=tracker is None)
+        if out is None:
+            out = torch.empty(x.shape[:-1] + (self.out_features,), dtype=x.dtype, device=x.device)
+            for a in range(0, self.out_features, self.rows):
+                b = min(a + self.rows, self.out_features)
+                w = dequantize_rows(self.weight[a:b], self.weight_scale[a:b], self.convrot, self.group_size,
+                                    dtype=torch.float32 if safe else torch.float16, check=tracker is None)
+                bias = None if self.bias is None else self.bias[a:b].to(x.dtype)
+                out[..., a:b] = F.linear(x, w, bias)
+                del w
         if tracker is not None:
             tracker.observe(self._ps_finite_slot, out)
         elif not torch.isfinite(out).all():
             raise FloatingPointError("NaN/Inf after the INT8 -> FP16 Linear")
         return out
+
+
+    def _native_forward(self, x, check):
+        """fp16 x [..., K] -> fp16 [..., N] on the gfx950 kernels, or None (and the tile path from
+        then on) when the kernels do not take the shape.  A missing library raises (as on the tile
+        path, whose GPU dequantization is a kernel too).  The dequantized weight's fp16 range check
+        of the tile path (dequantize_rows) is kept as a bound, once: every element of (q s) H^T is
+        at most sqrt(g) max|q s| in magnitude."""
+        from . import ops
+        if check and not getattr(self, "_ps_range_ok", False):
+            bound = (self.weight.abs().amax(dim=1, keepdim=True).float() * self.weight_scale.float().abs()).max()
+            if self.convrot:
+                bound = bound * self.group_size ** 0.5
+            if not torch.isfinite(bound) or bound > torch.finfo(torch.float16).max:
+                self._ps_native = False
+                return None
+            self._ps_range_ok = True
+        rows = x.reshape(-1, self.in_features).contiguous()
+        bias = None if self.bias is None else self.bias.to(torch.float16)
+        try:
+            xr = ops.rotate_rows(rows, self.group_size) if self.convrot else rows
+            y = ops.gemm_w8a16(xr, self.weight, self.weight_scale, bias, out_dtype=torch.float16)
+        except RuntimeError:
+            self._ps_native = False
+            return None
+        return y.reshape(x.shape[:-1] + (self.out_features,))
 
 
 def install_int8(model, quant, rows):

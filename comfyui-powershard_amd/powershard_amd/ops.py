@@ -108,6 +108,20 @@ def quantize_rows(x, fp8=False, rot_group=0, static_scale=None):
     return q, scale
 
 
+def rotate_rows(x, rot_group, out_dtype=None):
+    """x H per group of rot_group elements (the quantizer's fixed-order transform, one rounding to
+    out_dtype, default x.dtype).  x: [M, K] bf16/f16 on the GPU; rot_group 0 converts only."""
+    _need_gpu(x)
+    x = _rows2d(x)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"rotate_rows: activations must be bf16/f16, got {x.dtype}")
+    M, K = x.shape
+    y = torch.empty(M, K, dtype=out_dtype or x.dtype, device=x.device)
+    _launch("rotate_rows", _native.lib().psq_rotate_rows, _p(x), _DT[x.dtype], M, K, x.stride(0), int(rot_group or 0),
+            _p(y), _dt(y, "out"), K, _stream(x))
+    return y
+
+
 # ----------------------------------------------------------------------- GEMMs
 def gemm_i8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16):
     """y = round(fmaf(a @ w.T (int32), a_scale[m] * w_scale[n], bias[n])): [M, N] out_dtype."""

@@ -77,6 +77,15 @@ PSQ_API int psq_quantize_rows_fp8(const void *x, int x_dtype, int64_t M, int64_t
                           int rot_group, const float *static_scale, uint8_t *q, int64_t ldq,
                           float *scale, void *stream);
 
+/* Rotation only: y = round_out(x H) per group of rot_group elements, the same fixed-order fast
+ * transform in fp32 as above (H the normalized regular Hadamard), one rounding to y_dtype
+ * (bf16/f16/f32, ldy elements).  rot_group 0 converts only.  The activation side of the ConvRot
+ * int8 weight-only linear: x W^T = (x H)(q s)^T for weights stored as W H, so Int8Linear
+ * (powershard/operations.py:96-132, dequantize_rows 84-93) runs as psq_rotate_rows +
+ * psq_gemm_w8a16 instead of N/rows tile dequantizations.  K as above.  Bit-exact with the oracle. */
+PSQ_API int psq_rotate_rows(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int rot_group,
+                    void *y, int y_dtype, int64_t ldy, void *stream);
+
 /* ---------------------------------------------------------------------- GEMMs
  * W8A8: y[m][n] = round_out(fmaf((float)acc, a_scale[m] * w_scale[n], bias[n])),
  * acc = sum_k a[m][k] * w[n][k] in int32.  Replaces comfy-kitchen int8_linear behind

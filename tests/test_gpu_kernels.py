@@ -326,3 +326,16 @@ def test_dequant_fp8_bitexact(gpu):
     q, s = oracle.quantize_weight_fp8(w)
     got = ops.dequant_fp8(q.to(gpu), s.to(gpu), torch.float32)
     assert_bitexact(got, oracle.dequant_fp8(q, s, torch.float32), "fp8 dequant")
+
+
+# ----------------------------------------------------------------- rotation only
+@pytest.mark.parametrize("M,K,g", [(37, 512, 256), (5, 1024, 1024), (9, 256, 4), (3, 320, 16), (2, 4096, 64),
+                                   (4, 20480, 256), (6, 768, 0)])
+@pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                     (torch.float16, torch.float32), (torch.bfloat16, torch.float16)])
+def test_rotate_rows_bitexact(gpu, M, K, g, xdt, odt):
+    """x H per group (the quantizer's transform) rounded once to the output dtype."""
+    from powershard_amd import ops
+    x = heavy_rows(M, K, seed=K + M, dtype=xdt)
+    got = ops.rotate_rows(x.to(gpu), g, out_dtype=odt)
+    assert_bitexact(got, oracle.rotate_rows(x, g).to(odt), "rotate_rows")
