@@ -14,7 +14,9 @@ timed steps.  `cpu_baseline` is the CPU oracle (the quantized-reference restatem
 OpenMP) on a bounded sample of rows of the same workload, on this host's cores.
 
 `extra` carries the other shapes: the int4 (W4A16) text-encoder MLP at M=512 with an M sweep,
-the fp8 QKV projection, the 40-block Wan-14B linear stack, and the int8 weight-only layer.
+the fp8 QKV projection, the int8 weight-only layer, the Wan-14B FFN with its GELU in the
+up-projection's epilogue against the unfused reference sequence, and the 40-block Wan-14B linear
+stack.
 """
 import argparse
 import json
@@ -43,6 +45,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--extras", default="", help="comma-separated subset of the extra workloads to run "
+                    "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, wan14b_stack); default all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample time")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -313,6 +317,35 @@ def extra_wan_stack(args):
     return res
 
 
+def extra_ffn(args):
+    """Wan-14B FFN (powershard/wan_model.py:621-628) at M=32760: up 5120->13824, GELU(tanh), down
+    13824->5120, W8A8+ConvRot.  The reference sequence F.gelu(up(x).float()) -> down (fp32 hidden,
+    cast to bf16 by down) against the GELU in the up-projection's epilogue (up.forward_act)."""
+    import torch
+    import torch.nn.functional as Fn
+    M, D, F, cfg = 32760, 5120, 13824, 4
+    opts = {"convrot": True, "convrot_groupsize": 256}
+    up = quant_layer(D, F, "int8", cfg, seed=1000 + cfg + 5, opts=opts)[0]
+    down = quant_layer(F, D, "int8", cfg, seed=1000 + cfg + 6, opts=opts)[0]
+    x = activations(M, D, cfg, outlier_scale=50.0, student_t=True)
+    steps = max(3, min(args.steps, 10))
+    res = {"workload": "Wan-14B FFN up 5120->13824, GELU(tanh), down 13824->5120, W8A8+ConvRot, M=32760"}
+    with torch.no_grad():
+        res["unfused_ms"] = untimed_kernel_ms(lambda: down(Fn.gelu(up(x).float(), approximate="tanh")), steps, 1)
+        res["fused_ms"] = untimed_kernel_ms(lambda: down(up.forward_act(x)), steps, 1)
+        # the epilogue's cost: the up-projection alone, without and with the GELU
+        res["up_ms"] = untimed_kernel_ms(lambda: up(x), steps, 1)
+        res["up_gelu_ms"] = untimed_kernel_ms(lambda: up.forward_act(x), steps, 1)
+        ref = down(Fn.gelu(up(x).float(), approximate="tanh")).float()
+        got = down(up.forward_act(x)).float()
+        res["max_err_over_rms"] = ((got - ref).abs().max() / ref.pow(2).mean().sqrt()).item()
+    log(f"[bench] wan ffn: unfused {res['unfused_ms']:.3f} ms, fused {res['fused_ms']:.3f} ms; up GEMM "
+        f"{res['up_ms']:.3f} ms, with GELU {res['up_gelu_ms']:.3f} ms; max err/rms {res['max_err_over_rms']:.2e}")
+    del up, down, x
+    torch.cuda.empty_cache()
+    return res
+
+
 def extra_w8a16(args):
     import torch
     M, K, N, cfg = 1024, 5120, 5120, 0
@@ -378,7 +411,9 @@ def main():
     extra = {}
     if not args.no_extra:
         for name, fn in (("int4_w4a16", extra_int4), ("fp8", extra_fp8), ("w8a16", extra_w8a16),
-                         ("wan14b_stack", extra_wan_stack)):
+                         ("wan_ffn_gelu", extra_ffn), ("wan14b_stack", extra_wan_stack)):
+            if args.extras and name not in args.extras.split(","):
+                continue
             try:
                 extra[name] = fn(args)
             except torch.cuda.OutOfMemoryError as e:

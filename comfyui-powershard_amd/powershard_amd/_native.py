@@ -28,8 +28,10 @@ SIGNATURES = {
     "psq_quantize_rows_fp8": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P, _I64, _P, _P]),
     "psq_rotate_rows": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _I, _I64, _P]),
     "psq_gemm_i8": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
+    "psq_gemm_i8_act": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_i8_i32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_fp8": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
+    "psq_gemm_fp8_act": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_w4a16": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_w8a16": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_dequant_uint4": (_I, [_P, _P, _P, _I, _I64, _I64, _P, _I, _P]),

@@ -5,6 +5,9 @@
 //   y[m][n] = round_out(fmaf((float)acc[m][n], a_scale[m] * w_scale[n], bias[n]))
 //   int8: acc = sum_k a[m][k] w[n][k] in int32 (v_mfma_i32_32x32x32_i8, exact)
 //   fp8 : acc = the same in fp32 (v_mfma_f32_32x32x64_f8f6f4, e4m3 x e4m3)
+// With an epilogue activation (GELU, tanh form; the Wan FFN's F.gelu(fc1(x).float(),
+// approximate="tanh"), powershard/wan_model.py:626) the store writes round_out(act(round_out(y))):
+// the GELU of the rounded linear output, rounded to the dtype the next layer casts it to.
 //
 // Tiling (MI355X-first): a persistent grid of one workgroup per CU walks 256 x 256 output tiles;
 // a workgroup is 4 waves, one per SIMD (2 x 2, each wave 128 x 128 = 4 x 4 MFMA tiles of 32 x 32,
@@ -69,6 +72,39 @@ template <int OUT>
 __device__ __forceinline__ uint32_t pack2(float a, float b)
 {
     return pack_half2<OUT == OUT_BF16 ? PSQ_BF16 : PSQ_F16>(a, b);
+}
+
+// The epilogue's activation, applied to the output rounded to its dtype (fp32 outputs: unrounded);
+// the store rounds the result again.
+template <int OUT, int ACT>
+__device__ __forceinline__ float act1(float v)
+{
+    if constexpr (ACT == ACT_NONE || OUT == OUT_I32) return v;
+    else if constexpr (OUT == OUT_F32) return gelu_tanh(v);
+    else {
+        constexpr int DT = OUT == OUT_BF16 ? PSQ_BF16 : PSQ_F16;
+        return gelu_tanh(half_to_f32<DT>(f32_to_half<DT>(v)));
+    }
+}
+
+// Two outputs activated (as act1) and packed: the inner rounding is the same packed conversion.
+template <int OUT, int ACT>
+__device__ __forceinline__ uint32_t pack2a(float a, float b)
+{
+    if constexpr (ACT == ACT_NONE) {
+        return pack2<OUT>(a, b);
+    } else {
+        const uint32_t p = pack2<OUT>(a, b);
+        float ra, rb;
+        if constexpr (OUT == OUT_BF16) {
+            ra = __uint_as_float(p << 16);
+            rb = __uint_as_float(p & 0xffff0000u);
+        } else {
+            ra = f16_to_f32(p & 0xffffu);
+            rb = f16_to_f32(p >> 16);
+        }
+        return pack2<OUT>(gelu_tanh(ra), gelu_tanh(rb));
+    }
 }
 
 // One output element (the slow path of partial tiles and unaligned outputs).
@@ -178,7 +214,7 @@ __device__ __forceinline__ float bias_word(uint32_t w, int dt)
 // epilogue runs.  The MFMAs compute the transposed tile (W fragment as the first operand), which
 // gives each lane one output row and, per 32 x 32 tile, four runs of 4 consecutive columns: the
 // epilogue converts the accumulators in registers and stores them directly.
-template <bool FP8, int OUT>
+template <bool FP8, int OUT, int ACT>
 __global__ void __launch_bounds__(NTHREADS, 1)
 gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W, int64_t ldw,
                int M, int N, int K, Epi ep)
@@ -389,8 +425,8 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                                 for (int hh = 0; hh < 2; hh++) {
                                     uint32_t *o = hh == 0 ? x : y;
                                     const int r = 8 * pr + 4 * hh;
-                                    o[0] = pack2<OUT>(value(i, j, r, ws[hh][0], bs[hh][0]), value(i, j, r + 1, ws[hh][1], bs[hh][1]));
-                                    o[1] = pack2<OUT>(value(i, j, r + 2, ws[hh][2], bs[hh][2]), value(i, j, r + 3, ws[hh][3], bs[hh][3]));
+                                    o[0] = pack2a<OUT, ACT>(value(i, j, r, ws[hh][0], bs[hh][0]), value(i, j, r + 1, ws[hh][1], bs[hh][1]));
+                                    o[1] = pack2a<OUT, ACT>(value(i, j, r + 2, ws[hh][2], bs[hh][2]), value(i, j, r + 3, ws[hh][3], bs[hh][3]));
                                 }
                                 uint32_t lo[2], hi[2];
 #pragma unroll
@@ -452,10 +488,10 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                                 for (int c = 0; c < 4; c++) o[c] = (uint32_t)raw(i, j, r + c);
                             } else if constexpr (OUT == OUT_F32) {
 #pragma unroll
-                                for (int c = 0; c < 4; c++) o[c] = __float_as_uint(value(i, j, r + c, ws[h][c], bs[h][c]));
+                                for (int c = 0; c < 4; c++) o[c] = __float_as_uint(act1<OUT, ACT>(value(i, j, r + c, ws[h][c], bs[h][c])));
                             } else {
-                                o[0] = pack2<OUT>(value(i, j, r, ws[h][0], bs[h][0]), value(i, j, r + 1, ws[h][1], bs[h][1]));
-                                o[1] = pack2<OUT>(value(i, j, r + 2, ws[h][2], bs[h][2]), value(i, j, r + 3, ws[h][3], bs[h][3]));
+                                o[0] = pack2a<OUT, ACT>(value(i, j, r, ws[h][0], bs[h][0]), value(i, j, r + 1, ws[h][1], bs[h][1]));
+                                o[1] = pack2a<OUT, ACT>(value(i, j, r + 2, ws[h][2], bs[h][2]), value(i, j, r + 3, ws[h][3], bs[h][3]));
                             }
                         }
                         uint32_t lo[NW], hi[NW];
@@ -497,7 +533,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                         for (int c = 0; c < 4; c++) {
                             if (!live[i] || c >= n_left0 - nc) continue;
                             if constexpr (OUT == OUT_I32) ((int32_t *)p)[c] = raw(i, j, 4 * g + c);
-                            else store1<OUT>(p, c, value(i, j, 4 * g + c, ws[c], bs[c]));
+                            else store1<OUT>(p, c, act1<OUT, ACT>(value(i, j, 4 * g + c, ws[c], bs[c])));
                         }
                     }
                     __builtin_amdgcn_sched_barrier(0);
@@ -626,11 +662,11 @@ int cu_count(int dev)
     return cus[dev];
 }
 
-template <bool FP8, int OUT>
+template <bool FP8, int OUT, int ACT>
 int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                const Epi &ep, hipStream_t st, const char *name)
 {
-    auto kern = gemm_q8_kernel<FP8, OUT>;
+    auto kern = gemm_q8_kernel<FP8, OUT, ACT>;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
     static bool attr_set[64] = {};   // per device; the attribute is idempotent
@@ -650,14 +686,21 @@ int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int
 }
 
 template <bool FP8>
-int launch(int out, const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N, int64_t K,
-           const Epi &ep, hipStream_t st, const char *name)
+int launch(int out, int act, const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N,
+           int64_t K, const Epi &ep, hipStream_t st, const char *name)
 {
+    if (act == ACT_GELU_TANH) {
+        switch (out) {
+        case OUT_BF16: return launch_one<FP8, OUT_BF16, ACT_GELU_TANH>(a, lda, w, ldw, M, N, K, ep, st, name);
+        case OUT_F16: return launch_one<FP8, OUT_F16, ACT_GELU_TANH>(a, lda, w, ldw, M, N, K, ep, st, name);
+        default: return launch_one<FP8, OUT_F32, ACT_GELU_TANH>(a, lda, w, ldw, M, N, K, ep, st, name);
+        }
+    }
     switch (out) {
-    case OUT_BF16: return launch_one<FP8, OUT_BF16>(a, lda, w, ldw, M, N, K, ep, st, name);
-    case OUT_F16: return launch_one<FP8, OUT_F16>(a, lda, w, ldw, M, N, K, ep, st, name);
-    case OUT_F32: return launch_one<FP8, OUT_F32>(a, lda, w, ldw, M, N, K, ep, st, name);
-    default: return launch_one<FP8, OUT_I32>(a, lda, w, ldw, M, N, K, ep, st, name);
+    case OUT_BF16: return launch_one<FP8, OUT_BF16, ACT_NONE>(a, lda, w, ldw, M, N, K, ep, st, name);
+    case OUT_F16: return launch_one<FP8, OUT_F16, ACT_NONE>(a, lda, w, ldw, M, N, K, ep, st, name);
+    case OUT_F32: return launch_one<FP8, OUT_F32, ACT_NONE>(a, lda, w, ldw, M, N, K, ep, st, name);
+    default: return launch_one<FP8, OUT_I32, ACT_NONE>(a, lda, w, ldw, M, N, K, ep, st, name);
     }
 }
 
@@ -689,20 +732,29 @@ int check_shapes(const char *name, const void *a, int64_t lda, const void *w, in
 
 extern "C" {
 
-int psq_gemm_i8(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w, int64_t ldw,
-                const float *w_scale, const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,
-                int64_t M, int64_t N, int64_t K, void *stream)
+int psq_gemm_i8_act(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w, int64_t ldw,
+                    const float *w_scale, const void *bias, int bias_dtype, int activation, void *y, int y_dtype,
+                    int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
 {
     using namespace psq;
     if (int e = check_shapes("gemm_i8", a, lda, w, ldw, M, N, K)) return e;
+    if (activation != ACT_NONE && activation != ACT_GELU_TANH) return set_error(PSQ_E_ARG, "gemm_i8: bad activation");
     if (M == 0 || N == 0) return PSQ_OK;
     if (!a_scale || !w_scale || !y) return set_error(PSQ_E_ARG, "gemm_i8: null scale or output");
     if (!valid_dtype(y_dtype) || (bias && !valid_dtype(bias_dtype))) return set_error(PSQ_E_ARG, "gemm_i8: bad dtype");
     if (ldy < N) return set_error(PSQ_E_SHAPE, "gemm_i8: ldy < N");
     if (int e = require_device()) return e;
     Epi ep{a_scale, w_scale, 1, bias, bias_dtype, y, ldy, vec_ok(y, ldy, y_dtype == PSQ_F32 ? 4 : 2)};
-    return launch<false>(y_dtype, (const uint8_t *)a, lda, (const uint8_t *)w, ldw, M, N, K, ep,
+    return launch<false>(y_dtype, activation, (const uint8_t *)a, lda, (const uint8_t *)w, ldw, M, N, K, ep,
                          (hipStream_t)stream, "gemm_i8");
+}
+
+int psq_gemm_i8(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w, int64_t ldw,
+                const float *w_scale, const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,
+                int64_t M, int64_t N, int64_t K, void *stream)
+{
+    return psq_gemm_i8_act(a, lda, a_scale, w, ldw, w_scale, bias, bias_dtype, PSQ_ACT_NONE, y, y_dtype, ldy, M, N,
+                           K, stream);
 }
 
 int psq_gemm_i8_i32(const int8_t *a, int64_t lda, const int8_t *w, int64_t ldw, int32_t *c, int64_t ldc,
@@ -715,23 +767,32 @@ int psq_gemm_i8_i32(const int8_t *a, int64_t lda, const int8_t *w, int64_t ldw, 
     if (ldc < N) return set_error(PSQ_E_SHAPE, "gemm_i8_i32: ldc < N");
     if (int e = require_device()) return e;
     Epi ep{nullptr, nullptr, 0, nullptr, 0, c, ldc, vec_ok(c, ldc, 4)};
-    return launch<false>(OUT_I32, (const uint8_t *)a, lda, (const uint8_t *)w, ldw, M, N, K, ep,
+    return launch<false>(OUT_I32, ACT_NONE, (const uint8_t *)a, lda, (const uint8_t *)w, ldw, M, N, K, ep,
                          (hipStream_t)stream, "gemm_i8_i32");
 }
 
-int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, const uint8_t *w, int64_t ldw,
-                 const float *w_scale, int w_scale_per_row, const void *bias, int bias_dtype, void *y, int y_dtype,
-                 int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
+int psq_gemm_fp8_act(const uint8_t *a, int64_t lda, const float *a_scale, const uint8_t *w, int64_t ldw,
+                     const float *w_scale, int w_scale_per_row, const void *bias, int bias_dtype, int activation,
+                     void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
 {
     using namespace psq;
     if (int e = check_shapes("gemm_fp8", a, lda, w, ldw, M, N, K)) return e;
+    if (activation != ACT_NONE && activation != ACT_GELU_TANH) return set_error(PSQ_E_ARG, "gemm_fp8: bad activation");
     if (M == 0 || N == 0) return PSQ_OK;
     if (!a_scale || !w_scale || !y) return set_error(PSQ_E_ARG, "gemm_fp8: null scale or output");
     if (!valid_dtype(y_dtype) || (bias && !valid_dtype(bias_dtype))) return set_error(PSQ_E_ARG, "gemm_fp8: bad dtype");
     if (ldy < N) return set_error(PSQ_E_SHAPE, "gemm_fp8: ldy < N");
     if (int e = require_device()) return e;
     Epi ep{a_scale, w_scale, w_scale_per_row ? 1 : 0, bias, bias_dtype, y, ldy, vec_ok(y, ldy, y_dtype == PSQ_F32 ? 4 : 2)};
-    return launch<true>(y_dtype, a, lda, w, ldw, M, N, K, ep, (hipStream_t)stream, "gemm_fp8");
+    return launch<true>(y_dtype, activation, a, lda, w, ldw, M, N, K, ep, (hipStream_t)stream, "gemm_fp8");
+}
+
+int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, const uint8_t *w, int64_t ldw,
+                 const float *w_scale, int w_scale_per_row, const void *bias, int bias_dtype, void *y, int y_dtype,
+                 int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
+{
+    return psq_gemm_fp8_act(a, lda, a_scale, w, ldw, w_scale, w_scale_per_row, bias, bias_dtype, PSQ_ACT_NONE, y,
+                            y_dtype, ldy, M, N, K, stream);
 }
 
 }  // extern "C"

@@ -128,6 +128,22 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x)
     return sign | code;
 }
 
+// ------------------------------------------------------------------ activations
+// GELU, tanh approximation: gelu(x) = x (1 + tanh z) / 2 with z = sqrt(2/pi) (x + 0.044715 x^3).
+// (1 + tanh z) / 2 is the logistic function of 2 z, so gelu(x) = x / (1 + 2^(x (k0 + k1 x^2)))
+// with k0 = -2 sqrt(2/pi) log2(e), k1 = 0.044715 k0: the same function without the cancellation
+// of 1 + tanh z for negative x.  v_exp_f32 and v_rcp_f32 (about 1 ulp each).  Saturates to x for
+// large x and to -0 for large negative x; +-inf and NaN give what the tanh form gives.
+__device__ __forceinline__ float gelu_tanh(float x)
+{
+    constexpr float k0 = (float)(-2.0 * 0.79788456080286535588 * 1.44269504088896340736);
+    constexpr float k1 = (float)(-2.0 * 0.79788456080286535588 * 1.44269504088896340736 * 0.044715);
+    const float w = x * __builtin_fmaf(x * x, k1, k0);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(w));
+}
+
+enum { ACT_NONE = PSQ_ACT_NONE, ACT_GELU_TANH = PSQ_ACT_GELU_TANH };
+
 // ------------------------------------------------------------------ stores
 // Store one fp32 value as element i of an output of dtype dt.
 __device__ __forceinline__ void store_elem(void *p, int64_t i, int dt, float v)

@@ -1,0 +1,48 @@
+"""Linear -> GELU(tanh) -> Linear over token chunks with the GELU fused into the up-projection.
+
+Host side of the Wan FFN (powershard/wan_model.py:584-630, ``ffn_forward`` / ``chunked_mlp``).
+Per chunk of token rows the reference computes
+
+    hidden = F.gelu(fc1(rows).float(), approximate="tanh")     # fp32 [rows, hidden]
+    result[a:b] = fc2(hidden).float()                          # fc2 first casts hidden to bf16
+
+and so moves the hidden activation through HBM four times (fc1's bf16 output, its fp32 copy, the
+fp32 GELU, fc2's bf16 cast).  Here fc1's W8A8 / FP8 GEMM applies the GELU to its rounded output in
+the epilogue and writes the bf16 values fc2's cast would produce, once (QuantLinear.forward_act).
+The reference's memory planner (``mlp_plan`` / ``mlp_budget``, chunk sizing from an allocator
+budget) is not part of this package: ``chunk_tokens`` fixes the chunk size, None = one chunk.
+"""
+import torch
+import torch.nn.functional as F
+
+from .quant_linear import QuantLinear
+
+__all__ = ["gelu_linear", "chunked_mlp"]
+
+
+def gelu_linear(linear, rows):
+    """gelu_tanh(linear(rows)): fused for a QuantLinear (compute dtype), else the reference's fp32."""
+    if isinstance(linear, QuantLinear):
+        return linear.forward_act(rows, "gelu_tanh")
+    return F.gelu(linear(rows).float(), approximate="tanh")
+
+
+def chunked_mlp(fc1, fc2, x, chunk_tokens=None):
+    """fc2(gelu_tanh(fc1(x))) in fp32, computed over chunks of ``chunk_tokens`` token rows.
+
+    Follows wan_model.py:589-630: the result is fp32 [..., fc2.out_features]; each chunk's rows
+    are independent, so the chunk size does not change any value.
+    """
+    shape = x.shape
+    rows = x.reshape(-1, shape[-1])
+    n = rows.shape[0]
+    if chunk_tokens is not None and int(chunk_tokens) <= 0:
+        raise ValueError("chunk_tokens must be positive")
+    step = max(n, 1) if chunk_tokens is None else int(chunk_tokens)
+    result = torch.empty((n, fc2.out_features), dtype=torch.float32, device=x.device)
+    for a in range(0, n, step):
+        b = min(a + step, n)
+        hidden = gelu_linear(fc1, rows[a:b])
+        result[a:b] = fc2(hidden).float()
+        del hidden
+    return result.reshape(shape[:-1] + (fc2.out_features,))

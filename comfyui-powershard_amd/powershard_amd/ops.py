@@ -123,8 +123,23 @@ def rotate_rows(x, rot_group, out_dtype=None):
 
 
 # ----------------------------------------------------------------------- GEMMs
-def gemm_i8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16):
-    """y = round(fmaf(a @ w.T (int32), a_scale[m] * w_scale[n], bias[n])): [M, N] out_dtype."""
+# epilogue activations of the W8A8 / FP8 GEMMs (enum psq_activation)
+ACTIVATIONS = {None: 0, "none": 0, "gelu_tanh": 1}
+
+
+def _act(activation):
+    try:
+        return ACTIVATIONS[activation]
+    except KeyError:
+        raise ValueError(f"unknown epilogue activation {activation!r}") from None
+
+
+def gemm_i8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activation=None):
+    """y = round(fmaf(a @ w.T (int32), a_scale[m] * w_scale[n], bias[n])): [M, N] out_dtype.
+
+    activation "gelu_tanh": y = round(gelu_tanh(round(...))) -- the GELU of the rounded output,
+    rounded again (the Wan FFN's F.gelu(fc1(x).float(), approximate="tanh") then fc2's cast).
+    """
     _need_gpu(a, a_scale, w, w_scale)
     a, w = _rows2d(a), _rows2d(w)
     if a.dtype != torch.int8 or w.dtype != torch.int8:
@@ -139,8 +154,13 @@ def gemm_i8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16):
         raise ValueError("gemm_i8: scale sizes do not match M / N")
     bias, bdt = _bias(bias, N, a.device)
     y = torch.empty(M, N, dtype=out_dtype, device=a.device)
-    _launch("gemm_i8", _native.lib().psq_gemm_i8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale), _p(bias),
-                                            bdt, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
+    act = _act(activation)
+    if act:
+        _launch("gemm_i8", _native.lib().psq_gemm_i8_act, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale),
+                _p(bias), bdt, act, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
+    else:
+        _launch("gemm_i8", _native.lib().psq_gemm_i8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale),
+                _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
     return y
 
 
@@ -155,8 +175,11 @@ def gemm_i8_i32(a, w):
     return c
 
 
-def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16):
-    """fp8 e4m3fn GEMM: y = round(fmaf(a @ w.T (fp32), a_scale[m] * w_scale[n or 0], bias[n]))."""
+def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activation=None):
+    """fp8 e4m3fn GEMM: y = round(fmaf(a @ w.T (fp32), a_scale[m] * w_scale[n or 0], bias[n])).
+
+    activation as in gemm_i8.
+    """
     _need_gpu(a, a_scale, w, w_scale)
     a, w = _rows2d(a), _rows2d(w)
     for t in (a, w):
@@ -172,9 +195,13 @@ def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16):
         raise ValueError("gemm_fp8: scale sizes do not match")
     bias, bdt = _bias(bias, N, a.device)
     y = torch.empty(M, N, dtype=out_dtype, device=a.device)
-    _launch("gemm_fp8", _native.lib().psq_gemm_fp8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale),
-                                             int(w_scale.numel() > 1), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K,
-                                             _stream(a))
+    act = _act(activation)
+    if act:
+        _launch("gemm_fp8", _native.lib().psq_gemm_fp8_act, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0),
+                _p(w_scale), int(w_scale.numel() > 1), _p(bias), bdt, act, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
+    else:
+        _launch("gemm_fp8", _native.lib().psq_gemm_fp8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0),
+                _p(w_scale), int(w_scale.numel() > 1), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
     return y
 
 

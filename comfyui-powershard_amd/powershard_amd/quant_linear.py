@@ -226,6 +226,22 @@ class QuantLinear(nn.Module):
         return f"{self.in_features}, {self.out_features}, format={self._ps_qplan.fmt}, native={self._ps_native}"
 
     def forward(self, x):
+        return self._forward(x, None)
+
+    def forward_act(self, x, activation="gelu_tanh"):
+        """gelu_tanh(self(x)) with the activation fused into the native GEMM's epilogue.
+
+        The reference applies it outside the linear, F.gelu(fc1(rows).float(),
+        approximate="tanh") (powershard/wan_model.py:626), and the next QuantLinear casts the fp32
+        result to its compute dtype first (quant_linear.py:197).  On the native W8A8 / FP8 path the
+        result comes back in the compute dtype: the values that cast gives, without the fp32
+        intermediate.  Elsewhere it is the reference's fp32 F.gelu of the forward's output.
+        """
+        if activation != "gelu_tanh":
+            raise ValueError(f"unsupported activation {activation!r}")
+        return self._forward(x, activation)
+
+    def _forward(self, x, activation):
         plan = self._ps_qplan
         shape = x.shape
         if self._ps_follow_input and not self._ps_native:
@@ -241,9 +257,11 @@ class QuantLinear(nn.Module):
         # The reference's V100 "FP16 safe" mode computes the dequantized GEMM with an FP32 result.
         safe = getattr(self, "_ps_safe", False) and dtype == torch.float16
         out = None
+        fused = False   # activation applied by native_linear
         if self._ps_native and not safe and not self._ps_full_precision:
             try:
-                out = native_linear(rows, qt, bias, plan.fmt, extras.get("input_scale"))
+                out = native_linear(rows, qt, bias, plan.fmt, extras.get("input_scale"), activation)
+                fused = activation is not None
             except torch.cuda.OutOfMemoryError:
                 raise
             except (NotImplementedError, RuntimeError, TypeError, ValueError) as error:
@@ -254,6 +272,8 @@ class QuantLinear(nn.Module):
             out = F.linear(rows.float(), qt.dequantize().float(), None if bias is None else bias.float())
         elif out is None:
             out = F.linear(rows, qt.dequantize().to(dtype), bias)
+        if activation is not None and not fused:
+            out = F.gelu(out.float(), approximate="tanh")
         out = out.reshape(shape[:-1] + (self.out_features,))
         if self._ps_follow_input and x.is_floating_point() and out.dtype != x.dtype:
             out = out.to(x.dtype)  # text encoder: the FP32 graph is not narrowed to bf16 by the native kernel
@@ -263,10 +283,11 @@ class QuantLinear(nn.Module):
         return out
 
 
-def native_linear(rows, qt, bias, fmt, input_scale=None):
+def native_linear(rows, qt, bias, fmt, input_scale=None, activation=None):
     """The native GEMM of one format on the gfx950 kernels (replaces F.linear(QuantizedTensor)).
 
-    rows [M, K] in the compute dtype on the GPU; returns [M, N] in rows.dtype.
+    rows [M, K] in the compute dtype on the GPU; returns [M, N] in rows.dtype.  activation
+    "gelu_tanh" returns gelu(y) rounded to rows.dtype, fused into the W8A8 / FP8 epilogues.
     """
     from . import ops
     if rows.device.type != "cuda":
@@ -275,12 +296,15 @@ def native_linear(rows, qt, bias, fmt, input_scale=None):
     if layout is qtm.Int8RowwiseLayout:
         group = p.convrot_groupsize if p.convrot else 0
         qx, a_scale = ops.quantize_rows(rows, fp8=False, rot_group=group, static_scale=input_scale)
-        return ops.gemm_i8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype)
+        return ops.gemm_i8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype, activation=activation)
     if layout is qtm.Float8ScaledLayout:
         qx, a_scale = ops.quantize_rows(rows, fp8=True, rot_group=0, static_scale=input_scale)
-        return ops.gemm_fp8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype)
+        return ops.gemm_fp8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype, activation=activation)
     if layout is qtm.UInt4GroupLayout:
-        return ops.gemm_w4a16(rows, qt._qdata, p.scale, p.zero, p.group_size, bias, out_dtype=rows.dtype)
+        out = ops.gemm_w4a16(rows, qt._qdata, p.scale, p.zero, p.group_size, bias, out_dtype=rows.dtype)
+        if activation is not None:   # weight-only GEMM: the activation stays a separate pass
+            out = F.gelu(out.float(), approximate="tanh").to(rows.dtype)
+        return out
     raise NotImplementedError(f"no native kernel for {fmt}")
 
 

@@ -109,6 +109,31 @@ PSQ_API int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, co
                  int bias_dtype, void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
                  int64_t K, void *stream);
 
+/* GEMM epilogue activations (the *_act entry points). */
+enum psq_activation {
+    PSQ_ACT_NONE = 0,
+    PSQ_ACT_GELU_TANH = 1   /* gelu(v) = v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))) / 2 */
+};
+
+/* W8A8 / FP8 GEMM with an activation fused into the epilogue:
+ *   y[m][n] = round_out(act(round_out(fmaf((float)acc, a_scale[m] * w_scale[n], bias[n]))))
+ * act in fp32 on the rounded linear output: the numerics of the Wan FFN's
+ * F.gelu(fc1(rows).float(), approximate="tanh") (powershard/wan_model.py:626, chunked_mlp
+ * 589-630) followed by the .to(compute dtype) of fc2's QuantLinear.forward
+ * (powershard/quant_linear.py:197), with the fp32 hidden never written: the up-projection writes
+ * the down-projection's input directly.  GELU is evaluated as v / (1 + exp(-2 z)), the same
+ * function as the tanh form; results agree with torch's F.gelu to one output ulp outside the
+ * range v < -4, where the fp32 tanh form itself loses its relative precision.  Arguments as in
+ * psq_gemm_i8 / psq_gemm_fp8; y_dtype bf16, f16 or f32 (f32: no inner rounding).
+ * activation PSQ_ACT_NONE gives exactly psq_gemm_i8 / psq_gemm_fp8. */
+PSQ_API int psq_gemm_i8_act(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w,
+                    int64_t ldw, const float *w_scale, const void *bias, int bias_dtype, int activation,
+                    void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream);
+PSQ_API int psq_gemm_fp8_act(const uint8_t *a, int64_t lda, const float *a_scale, const uint8_t *w,
+                     int64_t ldw, const float *w_scale, int w_scale_per_row, const void *bias,
+                     int bias_dtype, int activation, void *y, int y_dtype, int64_t ldy, int64_t M,
+                     int64_t N, int64_t K, void *stream);
+
 /* W4A16: uint4 asymmetric group weights dequantized in registers,
  * w = round_bf16((float(q) - float(zero)) * float(scale)), multiplied on bf16 MFMA with
  * fp32 accumulation; y = round_out(acc + bias).  Replaces the int4 F.linear dispatch
