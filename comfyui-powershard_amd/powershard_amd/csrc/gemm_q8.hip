@@ -440,15 +440,35 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                                 *(v4i *)(eb + frow * 128 + ((ch ^ chunk_xor(frow)) << 4)) =
                                     v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
                             }
+                        // all four reads first (one LDS round trip), then the stores; a block of
+                        // whole rows stores without per-row tests from a wave-uniform base plus a
+                        // 32-bit lane offset
+                        v4i val[4];
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             const int row = 8 * q + (lane >> 3), ch = lane & 7;
-                            const v4i val = *(const v4i *)(eb + row * 128 + ((ch ^ chunk_xor(row)) << 4));
-                            const int m = m0 + wm * WAVE_M + 32 * i + row;
-                            if (m < M) {
-                                v4i *dst = (v4i *)((uint8_t *)ep.y + ((int64_t)m * ep.ldy + n0 + wn * WAVE_N + 64 * hj + 8 * ch) * 2);
-                                if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val, dst);
-                                else *dst = val;
+                            val[q] = *(const v4i *)(eb + row * 128 + ((ch ^ chunk_xor(row)) << 4));
+                        }
+                        const int mb = m0 + wm * WAVE_M + 32 * i;   // first row of the block
+                        const int64_t ubase = ((int64_t)mb * ep.ldy + n0 + wn * WAVE_N + 64 * hj) * 2;
+                        if (mb + 32 <= M) {
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                const uint32_t loff = (uint32_t)(((8 * q + (lane >> 3)) * ep.ldy + 8 * (lane & 7)) * 2);
+                                v4i *dst = (v4i *)((uint8_t *)ep.y + ubase + loff);
+                                if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val[q], dst);
+                                else *dst = val[q];
+                            }
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                const int row = 8 * q + (lane >> 3);
+                                if (mb + row < M) {
+                                    const uint32_t loff = (uint32_t)((row * ep.ldy + 8 * (lane & 7)) * 2);
+                                    v4i *dst = (v4i *)((uint8_t *)ep.y + ubase + loff);
+                                    if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val[q], dst);
+                                    else *dst = val[q];
+                                }
                             }
                         }
                         __builtin_amdgcn_sched_barrier(0);
@@ -649,19 +669,6 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     wait_vmcnt<0>();
 }
 
-// CUs of each device (the persistent grid size), cached per device.
-int cu_count(int dev)
-{
-    static int cus[64] = {};
-    if (dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 template <bool FP8, int OUT, int ACT>
 int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                const Epi &ep, hipStream_t st, const char *name)
@@ -704,9 +711,11 @@ int launch(int out, int act, const uint8_t *a, int64_t lda, const uint8_t *w, in
     }
 }
 
+// Vector stores need 16-byte-aligned rows; the staged stores also address a 32-row block with a
+// 32-bit lane offset, which holds for ldy < 2^26.  Other outputs take the element-store path.
 int vec_ok(const void *y, int64_t ldy, int elem)
 {
-    return (((uintptr_t)y & 15) == 0 && (ldy * elem) % 16 == 0) ? 1 : 0;
+    return (((uintptr_t)y & 15) == 0 && (ldy * elem) % 16 == 0 && ldy < (1LL << 26)) ? 1 : 0;
 }
 
 int check_shapes(const char *name, const void *a, int64_t lda, const void *w, int64_t ldw, int64_t M, int64_t N,

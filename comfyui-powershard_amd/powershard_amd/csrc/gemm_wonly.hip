@@ -191,12 +191,13 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
 }
 
 // ------------------------------------------------------------------ tiled kernel (M > 64)
-// A 256 x 256 output tile per workgroup of 4 waves.  Wave w owns all 256 rows (tokens) and the
-// 64 weight rows (output columns) 64w .. 64w + 63: 8 x 2 MFMA tiles of 32 x 32 on
-// v_mfma_f32_32x32x16_bf16 / f16 with the accumulators in AGPRs.  So every weight element is
-// dequantized once per workgroup, by the one wave that multiplies it, for 256 rows.  K runs in
+// A BM x 256 output tile (BM = 256, or 128 when that fills more of the GPU) per workgroup of 4
+// waves.  Wave w owns all BM rows (tokens) and the 64 weight rows (output columns) 64w .. 64w + 63:
+// BM/32 x 2 MFMA tiles of 32 x 32 on v_mfma_f32_32x32x16_bf16 / f16 with the accumulators in
+// AGPRs.  So every weight element is dequantized once per workgroup, by the one wave that
+// multiplies it, for BM rows.  K runs in
 // stages of 64 through a 3-deep LDS ring filled by global->LDS loads: per stage the activations
-// (256 rows x 128 bytes, XOR-swizzled 16-byte chunks), the packed weights (256 rows x 32 bytes of
+// (BM rows x 128 bytes, XOR-swizzled 16-byte chunks), the packed weights (256 rows x 32 bytes of
 // nibbles, or 64 bytes of int8) and, for uint4, each weight row's group scale and zero (one
 // 32-bit word each, zero-extended fp16).  Inside a stage the MFMAs of k-step t run beside the
 // activation fragment reads and the weight dequantization of k-step t + 1; the stage's one
@@ -204,31 +205,45 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
 // dequantization.  Lane-half h of every fragment carries k = 32 h + 8 t .. + 7 of the stage in
 // k-step t, for both operands, so a lane's weights of a stage are 16 contiguous bytes of nibbles.
 namespace wt {
-constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int NSTAGE = 3;                          // two stages in flight
-constexpr int TM = 8, TN = 2;                      // 32 x 32 tiles per wave: 256 rows x 64 columns
+constexpr int BN = 256, BK = 64;
+constexpr int TN = 2;                              // 32 x 32 tiles per wave: BM rows x 64 columns
 constexpr int XROW = BK * 2;                       // activation bytes per row per stage
-constexpr int XBYTES = BM * XROW;                  // 32 KB
-constexpr int XDMA = XBYTES / 1024 / 4;            // activation loads per wave per stage (8)
+template <int BM> constexpr int xbytes() { return BM * XROW; }                        // 32 / 16 KB
+template <int BM> constexpr int xdma() { return xbytes<BM>() / 1024 / 4; }            // activation loads per wave (8 / 4)
 template <int WK> constexpr int wrow() { return WK == W_UINT4 ? BK / 2 : BK; }         // 32 / 64 B
 template <int WK> constexpr int wdma() { return BN * wrow<WK>() / 1024 / 4; }          // 2 / 4
 template <int WK> constexpr int szdma() { return WK == W_UINT4 ? 2 : 0; }
-template <int WK> constexpr int lps() { return XDMA + wdma<WK>() + szdma<WK>(); }      // 12 / 12
-template <int WK> constexpr int slot_bytes() { return XBYTES + BN * wrow<WK>() + (WK == W_UINT4 ? 2 * BN * 4 : 0); }
-template <int WK> constexpr int lds_bytes() { return NSTAGE * slot_bytes<WK>(); }      // 126 / 144 KB
+template <int WK, int BM> constexpr int lps() { return xdma<BM>() + wdma<WK>() + szdma<WK>(); }   // 12 / 12 (BM 256)
+template <int WK, int BM> constexpr int slot_bytes() { return xbytes<BM>() + BN * wrow<WK>() + (WK == W_UINT4 ? 2 * BN * 4 : 0); }
+#ifndef PSQ_WT_NS128
+#define PSQ_WT_NS128 3
+#endif
+// ring depth: 3 slots of 256-row stages; up to PSQ_WT_NS128 of the half-size 128-row ones
+template <int WK, int BM> constexpr int nstage()
+{
+    return BM == 256 ? 3 : (163840 / slot_bytes<WK, BM>() < PSQ_WT_NS128 ? 163840 / slot_bytes<WK, BM>() : PSQ_WT_NS128);
+}
+template <int WK, int BM> constexpr int lds_bytes() { return nstage<WK, BM>() * slot_bytes<WK, BM>(); }   // 126 / 144 KB (BM 256)
 // activation chunk swizzle: bijective on 8 consecutive rows (32 banks) and on each parity class
 // of 16 consecutive rows (64 banks), so a fragment read (32 rows, one logical chunk) is conflict free
 __device__ __forceinline__ int xsw(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
 }  // namespace wt
 
-template <int XDT, int WK>
+template <int XDT, int WK, int BM>
 __global__ void __launch_bounds__(NTHREADS, 1)
 gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
 {
     using namespace wt;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
-    constexpr int LPS = lps<WK>();
+    constexpr int TM = BM / 32;                    // 32-row MFMA tiles per wave
+    constexpr int XBYTES = xbytes<BM>(), XDMA = xdma<BM>();
+    constexpr int SLOT = slot_bytes<WK, BM>();
+    constexpr int NSTAGE = nstage<WK, BM>();       // ring slots: NSTAGE - 1 stages in flight
+    constexpr int LPS = lps<WK, BM>();
+    constexpr int NQ = TM * TN;                    // MFMAs per k-step
+    constexpr int PPS = 8 / (NQ / 2);              // weight pairs dequantized behind each odd MFMA
+    constexpr int LPK = (LPS + 2) / 3;             // refill loads behind each of the first three k-steps
     constexpr int RB = wrow<WK>();
     constexpr int WDMA = wdma<WK>();
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -264,7 +279,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     // stage's scale and zero words of the wave's 64 columns)
     auto issue_one = [&](int slot, int kt, auto qc) {
         constexpr int q = decltype(qc)::value;
-        uint8_t *sl = smem + slot * slot_bytes<WK>();
+        uint8_t *sl = smem + slot * SLOT;
         if constexpr (q < XDMA) {
             constexpr int b4 = q * 4;
             __builtin_amdgcn_global_load_lds((glb_ptr)(xb + (int64_t)kt * BK * 2 + xo[q]),
@@ -290,13 +305,14 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     // ---- fragments
     auto read_x = [&](int slot, int t, int i) -> XV {
         const int r = 32 * i + frow, c = 4 * h + t;
-        return __builtin_bit_cast(XV, *(const v4i *)(smem + slot * slot_bytes<WK>() + r * XROW + ((c ^ xsw(r)) << 4)));
+        return __builtin_bit_cast(XV, *(const v4i *)(smem + slot * SLOT + r * XROW + ((c ^ xsw(r)) << 4)));
     };
     // the lane's packed weights of a stage (its 32 k of each of its two columns) and, for uint4,
-    // the columns' group scale and zero
+    // the columns' group scale s and -z s: a weight is round_16(fmaf(q, s, -z s)), one VALU op
+    // (as in the streaming kernel)
     struct WRaw { v4i w[TN][RB / 32]; float s[TN], z[TN]; };
     auto read_w = [&](int slot, WRaw &r) {
-        const uint8_t *sl = smem + slot * slot_bytes<WK>() + XBYTES;
+        const uint8_t *sl = smem + slot * SLOT + XBYTES;
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int n = 64 * wave + 32 * j + frow;
@@ -304,7 +320,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
             if constexpr (WK == W_UINT4) {
                 r.s[j] = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
-                r.z[j] = f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n));
+                r.z[j] = -(f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n)) * r.s[j]);   // -z s
             } else {
                 r.s[j] = 1.0f;
                 r.z[j] = 0.0f;
@@ -318,7 +334,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             float q[2];
             q[0] = ubyte_to_f32(p & 0x0f0f0f0fu, e);           // even k: low nibble of byte e
             q[1] = ubyte_to_f32((p >> 4) & 0x0f0f0f0fu, e);    // odd k: high nibble
-            return pack2<XDT>((q[0] - r.z[j]) * r.s[j], (q[1] - r.z[j]) * r.s[j]);
+            return pack2<XDT>(__builtin_fmaf(q[0], r.s[j], r.z[j]), __builtin_fmaf(q[1], r.s[j], r.z[j]));
         } else {
             const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
             const int sh = 16 * (e & 1);
@@ -370,13 +386,22 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             ([&] {
                 constexpr int q = Q;
                 mfma(q >> 1, q & 1, wc[q & 1], xc[q >> 1]);
-                if constexpr ((q & 1) == 0) xn[q >> 1] = read_x(xslot, tn, q >> 1);
-                else hw[q >> 3][(q >> 1) & 3] = dq_pair(wraw, q >> 3, tn, (q >> 1) & 3);
-                if constexpr (fill_base >= 0 && (q & 3) == 3)
-                    issue_one(fill_slot, fill_kt, std::integral_constant<int, fill_base + (q >> 2)>{});
+                if constexpr ((q & 1) == 0) {
+                    xn[q >> 1] = read_x(xslot, tn, q >> 1);
+                } else {
+#pragma unroll
+                    for (int v = 0; v < PPS; v++) {
+                        const int pi = (q >> 1) * PPS + v;          // pair pi: column tile pi / 4, pair pi % 4
+                        hw[pi >> 2][pi & 3] = dq_pair(wraw, pi >> 2, tn, pi & 3);
+                    }
+                }
+                // the refill loads: LPK of them spread over the k-step, the last of each group
+                constexpr int per = NQ / LPK, u = q / per;
+                if constexpr (fill_base >= 0 && q % per == per - 1 && u < LPK && fill_base + u < LPS)
+                    issue_one(fill_slot, fill_kt, std::integral_constant<int, fill_base + u>{});
                 __builtin_amdgcn_sched_barrier(0);
             }(), ...);
-        }(std::make_integer_sequence<int, TM * TN>{});
+        }(std::make_integer_sequence<int, NQ>{});
 #pragma unroll
         for (int j = 0; j < TN; j++) wn[j] = __builtin_bit_cast(XV, v4i{(int)hw[j][0], (int)hw[j][1], (int)hw[j][2], (int)hw[j][3]});
     };
@@ -388,8 +413,8 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         const int nxt = rs == NSTAGE - 1 ? 0 : rs + 1;
         using I = std::integral_constant<int, 0>;
         kstep(std::integral_constant<int, 1>{}, I{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
-        kstep(std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{}, xb2, wb0, xa, wa0, rs, wr, fill, kfill);
-        kstep(std::integral_constant<int, 3>{}, std::integral_constant<int, 8>{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
+        kstep(std::integral_constant<int, 2>{}, std::integral_constant<int, LPK>{}, xb2, wb0, xa, wa0, rs, wr, fill, kfill);
+        kstep(std::integral_constant<int, 3>{}, std::integral_constant<int, 2 * LPK>{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
         // stage kt + 1 landed for every wave; nobody reads stage kt's slot any more
         wait_vmcnt<(NSTAGE - 2) * LPS>();
         stage_barrier();
@@ -740,12 +765,12 @@ void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t
 // for uint4, the groups hold whole 32-element lane runs); the tiled kernel takes the rest.
 constexpr int64_t SKINNY_MAX_M = 64;
 
-template <int XDT, int WK>
-int launch_tiled(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
-                 const char *name)
+template <int XDT, int WK, int BM>
+int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                    const char *name)
 {
-    auto kern = gemm_wonly_tiled<XDT, WK>;
-    constexpr int lds = wt::lds_bytes<WK>();
+    auto kern = gemm_wonly_tiled<XDT, WK, BM>;
+    constexpr int lds = wt::lds_bytes<WK, BM>();
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
     static bool attr_set[64] = {};   // per device; the attribute is idempotent
@@ -754,9 +779,25 @@ int launch_tiled(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K
             return set_error(PSQ_E_DEVICE, "%s: cannot reserve %d bytes of LDS", name, lds);
         attr_set[dev] = true;
     }
-    const int64_t tiles = ((M + wt::BM - 1) / wt::BM) * ((N + wt::BN - 1) / wt::BN);
+    const int64_t tiles = ((M + BM - 1) / BM) * ((N + wt::BN - 1) / wt::BN);
     kern<<<dim3((unsigned)tiles), dim3(NTHREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
     return check_launch(name);
+}
+
+#ifndef PSQ_WT_FILL
+#define PSQ_WT_FILL 1
+#endif
+// 128-row tiles when they still fit one wave of workgroups on the GPU (twice the tiles of the
+// 256-row ones, each with half the MFMA work and the same dequantization), else 256-row tiles.
+template <int XDT, int WK>
+int launch_tiled(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                 const char *name)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
+    const int64_t tiles128 = ((M + 127) / 128) * ((N + wt::BN - 1) / wt::BN);
+    if (tiles128 <= PSQ_WT_FILL * cu_count(dev)) return launch_tiled_bm<XDT, WK, 128>(x, ldx, M, N, K, wa, st, name);
+    return launch_tiled_bm<XDT, WK, 256>(x, ldx, M, N, K, wa, st, name);
 }
 
 template <int WK>

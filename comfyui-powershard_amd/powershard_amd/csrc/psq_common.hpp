@@ -24,6 +24,9 @@ int check_launch(const char *what);
 // Validates the current device (gfx950) once per device; 0 or PSQ_E_DEVICE.
 int require_device();
 
+// Compute units of device `dev` (256 if it cannot be queried), cached.
+int cu_count(int dev);
+
 inline bool valid_dtype(int dt) { return dt == PSQ_BF16 || dt == PSQ_F16 || dt == PSQ_F32; }
 
 // ------------------------------------------------------------------ vector types

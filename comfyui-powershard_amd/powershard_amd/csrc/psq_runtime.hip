@@ -51,6 +51,20 @@ int require_device()
     return PSQ_OK;
 }
 
+// CUs of each device (persistent grid sizes, wave-fill decisions), cached per device; the value
+// written by concurrent first calls is the same.
+int cu_count(int dev)
+{
+    static int cus[kMaxDevices] = {};
+    if (dev < 0 || dev >= kMaxDevices) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 }  // namespace psq
 
 extern "C" {

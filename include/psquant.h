@@ -122,8 +122,9 @@ enum psq_activation {
  * 589-630) followed by the .to(compute dtype) of fc2's QuantLinear.forward
  * (powershard/quant_linear.py:197), with the fp32 hidden never written: the up-projection writes
  * the down-projection's input directly.  GELU is evaluated as v / (1 + exp(-2 z)), the same
- * function as the tanh form; results agree with torch's F.gelu to one output ulp outside the
- * range v < -4, where the fp32 tanh form itself loses its relative precision.  Arguments as in
+ * function as the tanh form without its cancellation: results are within one output ulp of the
+ * exact function, and of torch's fp32 F.gelu up to 1e-6 absolute (the fp32 tanh form loses
+ * relative precision below v = -3); below v = -9.6 (|gelu| < 1e-37) they are -0.  Arguments as in
  * psq_gemm_i8 / psq_gemm_fp8; y_dtype bf16, f16 or f32 (f32: no inner rounding).
  * activation PSQ_ACT_NONE gives exactly psq_gemm_i8 / psq_gemm_fp8. */
 PSQ_API int psq_gemm_i8_act(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w,
@@ -139,9 +140,9 @@ PSQ_API int psq_gemm_fp8_act(const uint8_t *a, int64_t lda, const float *a_scale
  * fp32 accumulation; y = round_out(acc + bias).  Replaces the int4 F.linear dispatch
  * (powershard/quant_linear.py:239, weight-only formats) and matches the dequantize
  * branch F.linear(rows, qt.dequantize().to(bf16), bias) (quant_linear.py:219-220).
- * For M <= 64 with group_size a multiple of 128 the weight-streaming kernel forms
- * w = round_bf16(fmaf(q, scale, -(zero * scale))), which differs from the formula above by one
- * bf16 ulp on about 2^-16 of the weights; both are within the fp32-accumulation bar.
+ * The weight-streaming kernel (M <= 64, group_size a multiple of 128) and the tiled kernel
+ * (M > 64) form w = round_bf16(fmaf(q, scale, -(zero * scale))), which differs from the formula
+ * above by one bf16 ulp on about 2^-16 of the weights; both are within the fp32-accumulation bar.
  *   x [M, K] bf16 (ldx), wq [N, K/2] bytes (low nibble = even k), scale/zero [N, K/group]
  *   fp16, group_size a multiple of 64 dividing K. */
 PSQ_API int psq_gemm_w4a16(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq,
