@@ -177,7 +177,7 @@ enum : int {
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v)
 {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
 // value of lane ^ (m * L) for the three radix-4 partners at lane stride L in {1, 4}
@@ -197,29 +197,19 @@ __device__ __forceinline__ float lane_xor(float v)
     }
 }
 
-// wave-wide max of non-negative values
-__device__ __forceinline__ float wave_max(float v)
-{
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        float w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
-}
-
 // ------------------------------------------------------------------ radix-4 ConvRot stage
 // y_j = S - 2 x_{3-j} with S = (x0 + x1) + (x2 + x3): one stage of the unnormalized regular
-// Hadamard transform (H4[a][b] = -1 iff a + b == 3).
+// Hadamard transform (H4[a][b] = -1 iff a + b == 3).  S - 2 x is one fma (2 x is exact, so it is
+// the once-rounded difference), one VALU op per output.
 __device__ __forceinline__ void radix4(float &x0, float &x1, float &x2, float &x3)
 {
     float s01 = x0 + x1;
     float s23 = x2 + x3;
     float s = s01 + s23;
-    float y0 = s - 2.0f * x3;
-    float y1 = s - 2.0f * x2;
-    float y2 = s - 2.0f * x1;
-    float y3 = s - 2.0f * x0;
+    float y0 = __builtin_fmaf(-2.0f, x3, s);
+    float y1 = __builtin_fmaf(-2.0f, x2, s);
+    float y2 = __builtin_fmaf(-2.0f, x1, s);
+    float y3 = __builtin_fmaf(-2.0f, x0, s);
     x0 = y0; x1 = y1; x2 = y2; x3 = y3;
 }
 
@@ -230,7 +220,7 @@ __device__ __forceinline__ float radix4_lanes(float x)
     float t = x + lane_xor<L, 1>(x);   // x_{d} + x_{d^1}: (x0+x1) or (x2+x3), commutative
     float s = t + lane_xor<L, 2>(t);   // (x0+x1) + (x2+x3)
     float r = lane_xor<L, 3>(x);       // x_{3-d}
-    return s - 2.0f * r;
+    return __builtin_fmaf(-2.0f, r, s);
 }
 
 // ------------------------------------------------------------------ XCD-aware tile order

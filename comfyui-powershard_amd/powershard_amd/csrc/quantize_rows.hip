@@ -5,7 +5,7 @@
 // Conventions (bit-exact with the CPU oracle):
 //   u = T(x): unnormalized regular-Hadamard transform per group of g = 4^k elements
 //     (x H = 2^-k T(x), H from powershard/operations.py:72-81), radix-4 stages over base-4
-//     digits, least significant digit first, S = (x0 + x1) + (x2 + x3), y_j = S - 2 x_{3-j};
+//     digits, least significant digit first, S = (x0 + x1) + (x2 + x3), y_j = fmaf(-2, x_{3-j}, S);
 //   a = max |u| over the row; a == 0 -> s = 1, q = 0; else r = LIM / a, s = (a / LIM) 2^-k;
 //   static input scale: s = s_in, r = (1 / s_in) 2^-k;
 //   int8: q = clamp(rint(u r), -127, 127);  fp8: q = e4m3_rne(clamp(u r, -448, 448)).
@@ -40,6 +40,54 @@ __device__ __forceinline__ void to_f32(const v4i (&raw)[2], float (&v)[16])
         v[8 + 2 * i] = half_to_f32<DT>(b);
         v[8 + 2 * i + 1] = half_to_f32<DT>(b >> 16);
     }
+}
+
+// Largest |v| over the 16 values, NaNs ignored (fmax returns the other operand), as a tree.
+__device__ __forceinline__ float absmax16(const float (&v)[16])
+{
+    float m[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) m[j] = __builtin_fmaxf(__builtin_fabsf(v[2 * j]), __builtin_fabsf(v[2 * j + 1]));
+#pragma unroll
+    for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) m[j] = __builtin_fmaxf(m[j], m[j + w]);
+    return m[0];
+}
+
+// Wave-wide max of non-negative, non-NaN values: DPP within rows of 16 lanes, then the
+// gfx950 row swaps across rows (no LDS, no index arithmetic).
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    v = __builtin_fmaxf(v, dpp<DPP_QUAD_XOR1>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_QUAD_XOR2>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_ROW_HALF_MIRROR>(v));   // lane ^ 7: the other quad of the 8
+    v = __builtin_fmaxf(v, dpp<DPP_ROW_MIRROR>(v));        // lane ^ 15: the other 8 of the row
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);   // rows 0 <-> 1, 2 <-> 3
+    v = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);   // halves
+    return __builtin_fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// int8 code of u r: clamp to [-127, 127] (equal to clamping after rounding, the bounds being
+// integers), then + 1.5 * 2^23, which rounds to the nearest integer (ties to even) and leaves the
+// code's two's complement in the low byte of the sum.  A NaN clamps to -127, as fmax(NaN, -127)
+// does in the rounding-first order.
+__device__ __forceinline__ uint32_t i8_code_bits(float u)
+{
+    u = __builtin_fminf(__builtin_fmaxf(u, -127.0f), 127.0f);
+    return __float_as_uint(u + 12582912.0f);
+}
+
+// Low bytes of four words packed into one (v_perm_b32: byte selectors 0-3 pick from the second
+// operand, 4-7 from the first, 12 gives zero).
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3)
+{
+    const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // Unnormalized transform of the 16 values of this thread (in-thread digits) and of the
@@ -122,13 +170,8 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
         for (int rr = 0; rr < R; rr++) {
             float amax = 0.0f;
 #pragma unroll
-            for (int c = 0; c < P; c++)
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const float a = __builtin_fabsf(v[rr][c][j]);
-                    amax = a > amax ? a : amax;
-                }
-            amax = wave_max(amax);
+            for (int c = 0; c < P; c++) amax = __builtin_fmaxf(amax, absmax16(v[rr][c]));
+            amax = wave_max_dpp(amax);
             if ((t & 63) == 0) wave_amax[rr][t >> 6] = amax;
         }
         __syncthreads();
@@ -159,22 +202,21 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
             uint32_t packed[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                uint32_t word = 0;
+                if constexpr (FP8) {
+                    uint32_t word = 0;
 #pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    float u = v[rr][c][4 * i + b] * r[rr];
-                    uint32_t code;
-                    if constexpr (FP8) {
+                    for (int b = 0; b < 4; b++) {
+                        float u = v[rr][c][4 * i + b] * r[rr];
                         u = __builtin_fminf(__builtin_fmaxf(u, -448.0f), 448.0f);
-                        code = f32_to_e4m3(u);
-                    } else {
-                        u = __builtin_rintf(u);
-                        u = __builtin_fminf(__builtin_fmaxf(u, -127.0f), 127.0f);
-                        code = (uint32_t)(int32_t)u & 0xffu;
+                        word |= f32_to_e4m3(u) << (8 * b);
                     }
-                    word |= code << (8 * b);
+                    packed[i] = word;
+                } else {
+                    uint32_t cb[4];
+#pragma unroll
+                    for (int b = 0; b < 4; b++) cb[b] = i8_code_bits(v[rr][c][4 * i + b] * r[rr]);
+                    packed[i] = pack_low_bytes(cb[0], cb[1], cb[2], cb[3]);
                 }
-                packed[i] = word;
             }
             *(v4i *)(q + (int64_t)row * ldq + (int64_t)(c * T + t) * kElemsPerThread) =
                 v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};

@@ -14,7 +14,9 @@
  *    H4[a][b] = -1 iff a + b == 3 (powershard/operations.py:72-81).
  *    Fast transform T (unnormalized, so x H = 2^-k T(x)): one radix-4 stage per base-4
  *    digit, digit 0 (least significant) first.  Within a stage, S = (x0 + x1) + (x2 + x3)
- *    and y_j = S - 2*x_{3-j}, all in fp32.  The 2^-k normalization is folded into the
+ *    and y_j = S - 2*x_{3-j} rounded once (fmaf(-2, x_{3-j}, S); 2x is exact, so this is the
+ *    rounding of the two-step form wherever 2x does not overflow), all in fp32.  The 2^-k
+ *    normalization is folded into the
  *    scales below (multiplying by a power of two is exact).
  *  - int8 activation quantization per row (token), u = T(x) (or x when not rotated):
  *    a = max|u|; if a == 0: s = 1, q = 0; else r = 127 / a (fp32 IEEE division, once per
@@ -182,10 +184,10 @@ static void fwht4_group(float *v, int g, int k)
             float s01 = x0 + x1;
             float s23 = x2 + x3;
             float s = s01 + s23;
-            v[base]              = s - 2.0f * x3;
-            v[base + stride]     = s - 2.0f * x2;
-            v[base + 2 * stride] = s - 2.0f * x1;
-            v[base + 3 * stride] = s - 2.0f * x0;
+            v[base]              = fmaf(-2.0f, x3, s);
+            v[base + stride]     = fmaf(-2.0f, x2, s);
+            v[base + 2 * stride] = fmaf(-2.0f, x1, s);
+            v[base + 3 * stride] = fmaf(-2.0f, x0, s);
         }
     }
 }
