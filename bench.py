@@ -283,7 +283,8 @@ def extra_fp8(args):
 
 def extra_wan_stack(args):
     """40 Wan-14B blocks of W8A8+ConvRot linears at M=32760 (q, k, v, o, ffn up, ffn down);
-    heavy-tailed inputs (Student-t df=3, 1% channels x50); random-init int8 weights per block."""
+    heavy-tailed inputs (Student-t df=3, 1% channels x50); random-init int8 weights per block.
+    Four activation quantizations per block: q, k and v share theirs (reuse_quantized_inputs)."""
     import torch
     M, D, F, cfg = 32760, 5120, 13824, 4
     opts = {"convrot": True, "convrot_groupsize": 256}
@@ -300,10 +301,14 @@ def extra_wan_stack(args):
     x = activations(M, D, cfg, outlier_scale=50.0, student_t=True)
     h = activations(M, F, cfg + 100, outlier_scale=50.0, student_t=True)
 
+    from powershard_amd.quant_linear import reuse_quantized_inputs
+
     def step():
         with torch.no_grad():
             for q, k, v, o, up, down in blocks:
-                q(x); k(x); v(x); o(x); up(x); down(h)
+                with reuse_quantized_inputs():   # q, k, v quantize their common input once
+                    q(x); k(x); v(x)
+                o(x); up(x); down(h)
     steps = max(2, min(args.steps, 3))
     ms, per = timed_steps(step, steps, 1)
     ops_per_block = 2.0 * M * (4 * D * D + 2 * D * F)

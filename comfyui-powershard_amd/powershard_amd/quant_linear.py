@@ -23,9 +23,11 @@ torch._scaled_mm / w4a8 ops by the HIP kernels (``native_linear``):
 * float8_e4m3fn: per-token e4m3 quantize, then the fp8 MFMA GEMM;
 * int4_asym_group: weight-only GEMM with in-register uint4 dequantization (W4A16).
 """
+import contextlib
 import dataclasses
 import json
 import math
+import threading
 import warnings
 
 import torch
@@ -283,6 +285,45 @@ class QuantLinear(nn.Module):
         return out
 
 
+# ------------------------------------------------------------------ shared activation quantization
+_shared = threading.local()
+
+
+@contextlib.contextmanager
+def reuse_quantized_inputs():
+    """Within the block, native W8A8 / FP8 modules that receive the same activation tensor quantize
+    it once: the q, k and v projections of one attention input (three QuantLinear calls on the same
+    x in the reference's Wan block, each quantizing x itself) share one rotate + quantize pass.
+
+    A quantized input is reused only for the same storage, offset, shape, strides, dtype and
+    in-place version of the rows tensor, the same rotation group / format / static scale, and the
+    same stream; the cache holds a reference to the rows, so their memory cannot be reused while it
+    lives, and it is dropped when the block exits.  Values are those of the uncached path.
+    """
+    prev = getattr(_shared, "cache", None)
+    _shared.cache = {}
+    try:
+        yield
+    finally:
+        _shared.cache = prev
+
+
+def _quantize_input(rows, fp8, group, input_scale):
+    from . import ops
+    cache = getattr(_shared, "cache", None)
+    if cache is None:
+        return ops.quantize_rows(rows, fp8=fp8, rot_group=group, static_scale=input_scale)
+    key = (rows.data_ptr(), tuple(rows.shape), tuple(rows.stride()), rows.dtype, rows._version, bool(fp8),
+           int(group or 0), None if input_scale is None else (input_scale.data_ptr(), input_scale._version),
+           torch.cuda.current_stream(rows.device).cuda_stream)
+    hit = cache.get(key)
+    if hit is not None:
+        return hit[1], hit[2]
+    qx, sx = ops.quantize_rows(rows, fp8=fp8, rot_group=group, static_scale=input_scale)
+    cache[key] = (rows, qx, sx, input_scale)   # the references keep the keyed memory alive
+    return qx, sx
+
+
 def native_linear(rows, qt, bias, fmt, input_scale=None, activation=None):
     """The native GEMM of one format on the gfx950 kernels (replaces F.linear(QuantizedTensor)).
 
@@ -295,10 +336,10 @@ def native_linear(rows, qt, bias, fmt, input_scale=None, activation=None):
     layout, p = qt._layout_cls, qt._params
     if layout is qtm.Int8RowwiseLayout:
         group = p.convrot_groupsize if p.convrot else 0
-        qx, a_scale = ops.quantize_rows(rows, fp8=False, rot_group=group, static_scale=input_scale)
+        qx, a_scale = _quantize_input(rows, False, group, input_scale)
         return ops.gemm_i8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype, activation=activation)
     if layout is qtm.Float8ScaledLayout:
-        qx, a_scale = ops.quantize_rows(rows, fp8=True, rot_group=0, static_scale=input_scale)
+        qx, a_scale = _quantize_input(rows, True, 0, input_scale)
         return ops.gemm_fp8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype, activation=activation)
     if layout is qtm.UInt4GroupLayout:
         out = ops.gemm_w4a16(rows, qt._qdata, p.scale, p.zero, p.group_size, bias, out_dtype=rows.dtype)

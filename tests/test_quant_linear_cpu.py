@@ -379,3 +379,15 @@ def test_install_int8():
     assert isinstance(model[0], Int8Linear) and "1" in skipped
     with pytest.raises(ValueError):
         install_int8(nn.Sequential(nn.Conv1d(2, 2, 1)), {"0": {"convrot": False, "group_size": 256}}, 8)
+
+
+def test_reuse_quantized_inputs_nests_and_restores():
+    from powershard_amd.quant_linear import _shared, reuse_quantized_inputs
+    assert getattr(_shared, "cache", None) is None
+    with reuse_quantized_inputs():
+        outer = _shared.cache
+        outer["k"] = 1
+        with reuse_quantized_inputs():
+            assert _shared.cache == {}
+        assert _shared.cache is outer
+    assert _shared.cache is None

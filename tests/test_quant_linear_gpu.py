@@ -133,3 +133,38 @@ def test_follow_input_returns_input_dtype(gpu):
     qa, sa = oracle.quantize_rows_i8(x.to(torch.bfloat16), 256)
     ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, qt._qdata), sa, qt._params.scale, b)
     assert torch.equal(y.cpu(), ref.float())
+
+
+@pytest.mark.parametrize("weight_format,opts", [("int8", {"convrot": True, "convrot_groupsize": 256}), ("fp8", {})])
+def test_reuse_quantized_inputs(gpu, weight_format, opts):
+    """q, k, v on one input inside reuse_quantized_inputs(): one quantize launch, outputs identical
+    to the uncached calls; an in-place change of the input, another tensor or another stream
+    quantizes again."""
+    from powershard_amd import ops
+    from powershard_amd.quant_linear import reuse_quantized_inputs
+    K = 1024
+    layers = [make_layer(K, 512, weight_format, opts, torch.bfloat16, True, gpu, seed=40 + i)[0] for i in range(3)]
+    x = heavy_rows(300, K, seed=44).to(gpu)
+    ref = [l(x) for l in layers]
+    name = "quantize_rows_fp8" if weight_format == "fp8" else "quantize_rows_i8"
+    with ops.kernel_timer() as ev, reuse_quantized_inputs():
+        got = [l(x) for l in layers]
+        launches = len(ev.get(name, []))
+        x2 = x.clone()
+        got2 = layers[0](x2)                 # another tensor with equal values
+        x.mul_(2.0)                          # in place: version bump
+        got3 = layers[0](x)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            got4 = layers[1](x)
+        torch.cuda.current_stream().wait_stream(side)
+        total = len(ev.get(name, []))
+    assert launches == 1, launches
+    assert total == 4, total
+    for a, b in zip(got, ref):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(got2.view(torch.int16), ref[0].view(torch.int16))
+    with torch.no_grad():
+        assert torch.equal(got3.view(torch.int16), layers[0](x).view(torch.int16))
+        assert torch.equal(got4.view(torch.int16), layers[1](x).view(torch.int16))
