@@ -13,12 +13,15 @@
 // a workgroup is 4 waves, one per SIMD (2 x 2, each wave 128 x 128 = 4 x 4 MFMA tiles of 32 x 32,
 // accumulators in the AGPR half of the register file).  K runs in stages of 128 bytes -- one full
 // cache line of every row -- through a 2-slot LDS ring (2 x 64 KB) filled by direct global->LDS
-// loads (global_load_lds_dwordx4: no staging registers, no LDS write instructions); a stage loads
-// while the previous one computes, continuously across the tiles of a workgroup.  Fragments are
-// double-buffered in registers so the LDS reads of the next k-step overlap the MFMAs of the
-// current one; one barrier per stage.  The epilogue converts the accumulators in registers and
-// stores them without an LDS round trip while the next tile's first stage loads.  MFMA-bound:
-// 2 M N K ops per launch.
+// loads (no staging registers, no LDS write instructions); a stage loads while the previous one
+// computes, continuously across the tiles of a workgroup.  Fragments are double-buffered in
+// registers so the LDS reads of the next k-step overlap the MFMAs of the current one; one barrier
+// per stage.  In the steady state of a tile (pairs of stages with the ring slot known at compile
+// time) a k-step issues no address arithmetic: fragment reads use per-tile lane offsets plus
+// immediates, and the ring loads are buffer loads with the tile base in a descriptor, the k
+// offset as scalar offset and the lane's row offset as vector offset.  The epilogue converts the
+// accumulators in registers and stages 32 x 64 blocks through LDS for whole-line stores while the
+// next tile's first stage loads.  MFMA-bound: 2 M N K ops per launch.
 #include "psq_common.hpp"
 
 namespace psq {
@@ -120,11 +123,12 @@ constexpr size_t kRingBytes = NSTAGE * 2 * STAGE_BYTES;
 
 // Stage rows are 128 bytes = eight 16-byte chunks.  A fragment read touches 32 consecutive rows at
 // one logical chunk, 16 lanes (256 bytes, all 64 banks) per LDS cycle: bank group 8 (r & 1) +
-// physical chunk.  Chunk c of row r is stored at c ^ f(r), f(r) = (r ^ (r >> 3)) & 7, which is
-// bijective in row bits 0-2 (8 consecutive rows: distinct chunks) and, for a fixed bit 0, in bits
-// 1-3 (the 8 rows of one parity among 16 consecutive rows), so every read is conflict free.  fp8
+// physical chunk.  Chunk c of row r is stored at c ^ f(r), f(r) = (r0 ^ r3, r1 ^ r4, r2) in bits,
+// which is bijective in row bits 0-2 (8 consecutive rows: distinct chunks) and, for a fixed bit 0,
+// in bits 1-3 (the 8 rows of one parity among 16 consecutive rows), so every read is conflict
+// free.  f ignores row bit 5 and up, so the fragments of all 32-row blocks share one swizzle.  fp8
 // reads two consecutive chunks per lane, each its own conflict-free read.
-__device__ __forceinline__ int chunk_xor(int row) { return (row ^ (row >> 3)) & 7; }
+__device__ __forceinline__ int chunk_xor(int row) { return ((row ^ (row >> 3)) & 3) | (row & 4); }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ chunk_xor(row)) << 4); }
 
 // Ring-load schedule: dma_slot(t, p) is the ring load (0-15: A blocks, then W blocks) issued
@@ -219,7 +223,7 @@ __global__ void __launch_bounds__(NTHREADS, 1)
 gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W, int64_t ldw,
                int M, int N, int K, Epi ep)
 {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];   // ring [NSTAGE][A | W], scales
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];   // ring A[NSTAGE] | W[NSTAGE], scales
     using Acc = typename std::conditional<FP8, v16f, v16i>::type;
     using FT = typename Frag<FP8>::T;
     constexpr int KS = BK / Frag<FP8>::KSTEP;      // k-steps per stage: 4 (int8), 2 (fp8)
@@ -290,11 +294,28 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     // turned into a load from a selected address, which sends both arrays to scratch memory).
     auto issue_one = [&](int slot, bool same, int64_t koff, int q) {
         const int j = q % LOADS, b = j * (NTHREADS / 64) + wave;
-        lds_ptr d = (lds_ptr)(smem + slot * 2 * STAGE_BYTES + (q < LOADS ? 0 : STAGE_BYTES) + 1024 * b);
+        lds_ptr d = (lds_ptr)(smem + (q < LOADS ? 0 : NSTAGE * STAGE_BYTES) + slot * STAGE_BYTES + 1024 * b);
         const int32_t mask = same ? 0 : -1;
         const uint8_t *base = (q < LOADS ? (same ? ba : nba) : (same ? bw : nbw)) + koff;
         const uint32_t off = q < LOADS ? oa[j] + (uint32_t)(doa[j] & mask) : ow[j] + (uint32_t)(dow[j] & mask);
         __builtin_amdgcn_global_load_lds((glb_ptr)(base + off), d, 16, 0, 0);
+    };
+
+    // the same with the slot and load index known at compile time and the load from the current
+    // tile: the scalar base plus the lane's offset, no select
+    // (buffer form: the tile's operand base in a descriptor, the k offset as the scalar offset and
+    // the lane's row offset as the vector offset -- no address arithmetic per load)
+    __amdgpu_buffer_rsrc_t rsa, rsw;
+    auto set_rsrc = [&] {
+        rsa = __builtin_amdgcn_make_buffer_rsrc((void *)ba, (short)0, -1, 0x00020000);
+        rsw = __builtin_amdgcn_make_buffer_rsrc((void *)bw, (short)0, -1, 0x00020000);
+    };
+    auto issue_fast = [&](auto slotc, int64_t koff, auto qc) {
+        constexpr int slot = decltype(slotc)::value, q = decltype(qc)::value, j = q % LOADS;
+        const int b = j * (NTHREADS / 64) + wave;
+        lds_ptr d = (lds_ptr)(smem + (q < LOADS ? 0 : NSTAGE * STAGE_BYTES) + slot * STAGE_BYTES + 1024 * b);
+        if constexpr (q < LOADS) __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, d, 16, oa[j], (int)koff, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, d, 16, ow[j], (int)koff, 0, 0);
     };
 
     // MFMA operand layout (32 x 32 tiles): lane holds row (lane & 31) of W / of A and the k-slice
@@ -303,7 +324,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     const int frow = lane & 31, fk = lane >> 5;
     // fragment q of k-step ks of the stage in `slot`: q < TM is A fragment q, else W fragment q - TM
     auto read_frag = [&](int slot, int ks, int q, FT (&fa)[TM], FT (&fw)[TN]) {
-        const uint8_t *base = smem + slot * 2 * STAGE_BYTES + (q < TM ? 0 : STAGE_BYTES);
+        const uint8_t *base = smem + (q < TM ? 0 : NSTAGE * STAGE_BYTES) + slot * STAGE_BYTES;
         const int r = (q < TM ? wm * WAVE_M + q * 32 : wn * WAVE_N + (q - TM) * 32) + frow;
         if constexpr (FP8) {
             // the lane's 32 bytes are chunks 4 ks + 2 fk and + 1: two 16-byte reads (a 32-byte
@@ -316,6 +337,40 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         } else {
             const v4i f = *(const v4i *)(base + swz(r, 2 * ks + fk));
             if (q < TM) fa[q] = f;
+            else fw[q - TM] = f;
+        }
+    };
+    // Fragment reads with the slot known at compile time: the lane's swizzled byte offset depends
+    // only on the operand, the k-step and the read half (fp8), so 2 x KS x NH offsets per lane
+    // (set per tile, dead during the epilogue) cover every read; the slot and the fragment's
+    // 32-row block are immediates of the ds_read.
+    constexpr int KSC = BK / Frag<FP8>::KSTEP, NHC = FP8 ? 2 : 1;
+    uint32_t lof[2][KSC][NHC];
+    auto set_lof = [&] {
+#pragma unroll
+        for (int o = 0; o < 2; o++)
+#pragma unroll
+            for (int ks = 0; ks < KSC; ks++)
+#pragma unroll
+                for (int hh = 0; hh < NHC; hh++) {
+                    const int c = FP8 ? 4 * ks + 2 * fk + hh : 2 * ks + fk;
+                    lof[o][ks][hh] = (uint32_t)((o ? NSTAGE * STAGE_BYTES + wn * WAVE_N * BK : wm * WAVE_M * BK) +
+                                                frow * BK + ((c ^ chunk_xor(frow)) << 4));
+                }
+    };
+    auto read_frag_c = [&](auto slotc, auto ksc, auto qc, FT (&fa)[TM], FT (&fw)[TN]) {
+        constexpr int slot = decltype(slotc)::value, ks = decltype(ksc)::value, q = decltype(qc)::value;
+        constexpr int o = q < TM ? 0 : 1, ql = q < TM ? q : q - TM;
+        constexpr uint32_t imm = slot * STAGE_BYTES + ql * 32 * BK;
+        if constexpr (FP8) {
+            const v4i lo = *(const v4i *)(smem + lof[o][ks][0] + imm);
+            const v4i hi = *(const v4i *)(smem + lof[o][ks][1] + imm);
+            const v8i f = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if constexpr (q < TM) fa[q] = f;
+            else fw[q - TM] = f;
+        } else {
+            const v4i f = *(const v4i *)(smem + lof[o][ks][0] + imm);
+            if constexpr (q < TM) fa[q] = f;
             else fw[q - TM] = f;
         }
     };
@@ -608,6 +663,45 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             __builtin_amdgcn_sched_barrier(0);
         });
     };
+    // k-step / stage of the steady state: stage kt + 2 still in the current tile, ring slot SL
+    // known at compile time
+    auto kstep_fast = [&](auto tc, auto slc, FT (&ca)[TM], FT (&cw)[TN], FT (&na)[TM], FT (&nw)[TN], int64_t k1,
+                          int64_t k2) {
+        constexpr int t = decltype(tc)::value, SL = decltype(slc)::value;
+        constexpr bool last = t == KS - 1;
+        static_for<TM * TN>([&](auto pc) {
+            constexpr int p = decltype(pc)::value;
+            mfma(p / TN, p % TN, ca, cw);
+            if constexpr (p < TM + TN)
+                read_frag_c(std::integral_constant<int, last ? (SL ^ 1) : SL>{},
+                            std::integral_constant<int, last ? 0 : t + 1>{},
+                            std::integral_constant<int, kReadOrder[p]>{}, na, nw);
+            constexpr int d = dma_slot<FP8>(t, p);
+            if constexpr (d >= 0) {
+                if constexpr (last) issue_fast(std::integral_constant<int, SL>{}, k2, std::integral_constant<int, d>{});
+                else issue_fast(std::integral_constant<int, SL ^ 1>{}, k1, std::integral_constant<int, d>{});
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    auto stage_fast = [&](auto slc, int kt) {
+        const int64_t k1 = (int64_t)(kt + 1) * BK, k2 = (int64_t)(kt + 2) * BK;
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        if constexpr (!FP8) {
+            kstep_fast(I0{}, slc, fa0, fw0, fa1, fw1, k1, k2);
+            kstep_fast(I1{}, slc, fa1, fw1, fa0, fw0, k1, k2);
+            kstep_fast(std::integral_constant<int, 2>{}, slc, fa0, fw0, fa1, fw1, k1, k2);
+            wait_vmcnt<0>();
+            stage_barrier();
+            kstep_fast(std::integral_constant<int, 3>{}, slc, fa1, fw1, fa0, fw0, k1, k2);
+        } else {
+            kstep_fast(I0{}, slc, fa0, fw0, fa1, fw1, k1, k2);
+            wait_vmcnt<0>();
+            stage_barrier();
+            kstep_fast(I1{}, slc, fa1, fw1, fa0, fw0, k1, k2);
+        }
+    };
     auto stage = [&](int kt) {
         bool s1, s2;
         int64_t k1, k2;
@@ -650,8 +744,20 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        int kt0 = 0;
+        if ((nk & 1) == 0) {
+            set_lof();
+            set_rsrc();
+            // an even stage count brings the ring back to slot 0 at every tile start: the steady
+            // state runs in pairs of stages with compile-time slots, the last two the general way
 #pragma clang loop unroll(disable)
-        for (int kt = 0; kt < nk; kt++) stage(kt);
+            for (; kt0 + 3 < nk; kt0 += 2) {
+                stage_fast(std::integral_constant<int, 0>{}, kt0);
+                stage_fast(std::integral_constant<int, 1>{}, kt0 + 1);
+            }
+        }
+#pragma clang loop unroll(disable)
+        for (int kt = kt0; kt < nk; kt++) stage(kt);
         epilogue(m0, n0, buf);
         buf = buf == NSCALEBUF - 1 ? 0 : buf + 1;
         if (!has_next) break;
