@@ -41,7 +41,7 @@ namespace {
 #define PSQ_Q8_HOIST 1
 #endif
 #ifndef PSQ_Q8_DMA_I8
-#define PSQ_Q8_DMA_I8 1
+#define PSQ_Q8_DMA_I8 2
 #endif
 #ifndef PSQ_Q8_DMA_F8
 #define PSQ_Q8_DMA_F8 0
@@ -135,7 +135,8 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chu
 // behind MFMA p (0-15) of k-step t, or -1.  Loads behind the last k-step (after the barrier) fill
 // the slot just freed with stage kt + 2 and are numbered first; loads behind the earlier k-steps
 // complete stage kt + 1 in the other slot before the barrier.  The fragment reads of the next
-// k-step go behind MFMAs 0-7.
+// k-step go behind MFMAs 0-7.  int8 uses schedule 2: 6 loads behind the even MFMAs 2-12 of the
+// last k-step, 5 behind MFMAs 1, 4, 7, 10, 13 of k-steps 0 and 1 (measured 1% ahead of the others).
 template <bool FP8>
 constexpr int dma_slot(int t, int p)
 {
