@@ -52,6 +52,18 @@ def _compile(src):
     return obj
 
 
+def _check_stubs(lib):
+    """Fail on an undefined symbol of the library's own namespace.  When the host pass of a .hip
+    file rejects a kernel body (a target builtin it cannot check there), clang drops the kernel's
+    launch stub without an error, and the library then fails to load on the GPU host."""
+    r = subprocess.run(["nm", "-D", "--undefined-only", str(lib)], capture_output=True, text=True)
+    if r.returncode != 0:
+        return   # no binutils: the ABI test's load of the library still catches it
+    missing = [line.split()[-1] for line in r.stdout.splitlines() if "_ZN3psq" in line]
+    if missing:
+        raise RuntimeError("kernel launch stubs missing (host pass dropped them): " + ", ".join(missing[:4]))
+
+
 def build(jobs=None, verbose=False):
     """Compile every csrc/*.hip for gfx950 and link lib/libpsquant.so. Returns the library path."""
     BUILD.mkdir(exist_ok=True)
@@ -65,6 +77,7 @@ def build(jobs=None, verbose=False):
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    _check_stubs(tmp)
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

@@ -308,15 +308,15 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     // the lane's row offset as the vector offset -- no address arithmetic per load)
     __amdgpu_buffer_rsrc_t rsa, rsw;
     auto set_rsrc = [&] {
-        rsa = __builtin_amdgcn_make_buffer_rsrc((void *)ba, (short)0, -1, 0x00020000);
-        rsw = __builtin_amdgcn_make_buffer_rsrc((void *)bw, (short)0, -1, 0x00020000);
+        rsa = raw_rsrc(ba);
+        rsw = raw_rsrc(bw);
     };
     auto issue_fast = [&](auto slotc, int64_t koff, auto qc) {
         constexpr int slot = decltype(slotc)::value, q = decltype(qc)::value, j = q % LOADS;
         const int b = j * (NTHREADS / 64) + wave;
         lds_ptr d = (lds_ptr)(smem + (q < LOADS ? 0 : NSTAGE * STAGE_BYTES) + slot * STAGE_BYTES + 1024 * b);
-        if constexpr (q < LOADS) __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, d, 16, oa[j], (int)koff, 0, 0);
-        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, d, 16, ow[j], (int)koff, 0, 0);
+        if constexpr (q < LOADS) buffer_load_lds16(rsa, d, oa[j], (int)koff);
+        else buffer_load_lds16(rsw, d, ow[j], (int)koff);
     };
 
     // MFMA operand layout (32 x 32 tiles): lane holds row (lane & 31) of W / of A and the k-slice

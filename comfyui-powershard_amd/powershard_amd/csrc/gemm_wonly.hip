@@ -242,7 +242,6 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     constexpr int NSTAGE = nstage<WK, BM>();       // ring slots: NSTAGE - 1 stages in flight
     constexpr int LPS = lps<WK, BM>();
     constexpr int NQ = TM * TN;                    // MFMAs per k-step
-    constexpr int PPS = 8 / (NQ / 2);              // weight pairs dequantized behind each odd MFMA
     constexpr int LPK = (LPS + 2) / 3;             // refill loads behind each of the first three k-steps
     constexpr int RB = wrow<WK>();
     constexpr int WDMA = wdma<WK>();
@@ -275,6 +274,10 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     const unsigned spg = WK == W_UINT4 ? (unsigned)(wa.gs / BK) : 1u;   // stages per group
     const uint8_t *xb = (const uint8_t *)(x + (int64_t)m0 * ldx);
     const uint8_t *wb = wa.wq + (int64_t)n0 * wld;
+    // The tile's activation and weight rows as buffer descriptors: a load is the descriptor, the
+    // stage's k offset as scalar offset and the lane's row offset as vector offset (no per-load
+    // address arithmetic).
+    const __amdgpu_buffer_rsrc_t rsx = raw_rsrc(xb), rsw = raw_rsrc(wb);
     // load q of a stage (q < 8: activation block q; then weight blocks; then, for uint4, the
     // stage's scale and zero words of the wave's 64 columns)
     auto issue_one = [&](int slot, int kt, auto qc) {
@@ -282,12 +285,10 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         uint8_t *sl = smem + slot * SLOT;
         if constexpr (q < XDMA) {
             constexpr int b4 = q * 4;
-            __builtin_amdgcn_global_load_lds((glb_ptr)(xb + (int64_t)kt * BK * 2 + xo[q]),
-                                             (lds_ptr)(sl + 1024 * (b4 + wave)), 16, 0, 0);
+            buffer_load_lds16(rsx, (lds_ptr)(sl + 1024 * (b4 + wave)), xo[q], kt * BK * 2);
         } else if constexpr (q < XDMA + WDMA) {
             constexpr int j = q - XDMA;
-            __builtin_amdgcn_global_load_lds((glb_ptr)(wb + (int64_t)kt * RB + wo[j]),
-                                             (lds_ptr)(sl + XBYTES + 1024 * (j * 4 + wave)), 16, 0, 0);
+            buffer_load_lds16(rsw, (lds_ptr)(sl + XBYTES + 1024 * (j * 4 + wave)), wo[j], kt * RB);
         } else if constexpr (WK == W_UINT4) {
             constexpr bool zero = q == LPS - 1;
             const int64_t gi = (int64_t)scol * G + (int)((unsigned)kt / spg);   // the stage's group
@@ -386,15 +387,12 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             ([&] {
                 constexpr int q = Q;
                 mfma(q >> 1, q & 1, wc[q & 1], xc[q >> 1]);
-                if constexpr ((q & 1) == 0) {
-                    xn[q >> 1] = read_x(xslot, tn, q >> 1);
-                } else {
-#pragma unroll
-                    for (int v = 0; v < PPS; v++) {
-                        const int pi = (q >> 1) * PPS + v;          // pair pi: column tile pi / 4, pair pi % 4
-                        hw[pi >> 2][pi & 3] = dq_pair(wraw, pi >> 2, tn, pi & 3);
-                    }
-                }
+                if constexpr ((q & 1) == 0) xn[q >> 1] = read_x(xslot, tn, q >> 1);
+                // weight pair pi (column tile pi / 4, pair pi % 4): behind the odd MFMAs of a
+                // 16-MFMA k-step, behind every MFMA of an 8-MFMA one (7 VALU ops a pair, one MFMA's
+                // worth of issue slots)
+                constexpr int pi = NQ >= 16 ? ((q & 1) ? (q >> 1) : -1) : q;
+                if constexpr (pi >= 0) hw[pi >> 2][pi & 3] = dq_pair(wraw, pi >> 2, tn, pi & 3);
                 // the refill loads: LPK of them spread over the k-step, the last of each group
                 constexpr int per = NQ / LPK, u = q / per;
                 if constexpr (fill_base >= 0 && q % per == per - 1 && u < LPK && fill_base + u < LPS)
@@ -816,6 +814,7 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
         return check_launch(name);
     }
     if (ldx > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: ldx above 2^22", name);   // 32-bit row offsets
+    if (K > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: K above 2^22", name);       // (of the weights too)
     return x_dtype == PSQ_BF16 ? launch_tiled<PSQ_BF16, WK>(xp, ldx, M, N, K, wa, st, name)
                                : launch_tiled<PSQ_F16, WK>(xp, ldx, M, N, K, wa, st, name);
 }

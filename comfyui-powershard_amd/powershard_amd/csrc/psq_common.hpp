@@ -241,9 +241,24 @@ __device__ __forceinline__ void tile_order(int pid, int nbm, int nbn, int group_
     pn = r / gsz;
 }
 
+// ------------------------------------------------------------------ buffer descriptors
+// Raw buffer descriptor over `base` (no stride, no range limit, 32-bit data format): a buffer load
+// reads base + vector offset + scalar offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void *base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, -1, 0x00020000);
+}
+
 // ------------------------------------------------------------------ GEMM pipelines
 typedef __attribute__((address_space(3))) uint8_t *lds_ptr;
 typedef const __attribute__((address_space(1))) void *glb_ptr;
+
+// Global -> LDS load through a buffer descriptor: 16 bytes per lane from descriptor base + voff +
+// soff into dst + 16 * lane (dst wave-uniform; it goes to M0).
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rs, lds_ptr dst, uint32_t voff, int soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, voff, soff, 0, 0);
+}
 
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4]<<14)
 template <int N>
