@@ -111,26 +111,6 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c)
     return (c & 0x80u) ? -v : v;
 }
 
-// OCP e4m3fn encode, round to nearest even, saturating to +-448 (callers clamp first).
-__device__ __forceinline__ uint32_t f32_to_e4m3(float x)
-{
-    uint32_t u = __float_as_uint(x);
-    uint32_t sign = (u >> 24) & 0x80u;
-    uint32_t au = u & 0x7fffffffu;
-    float a = __uint_as_float(au);
-    uint32_t code;
-    if (au > 0x7f800000u) return 0x7fu;
-    if (a >= 448.0f) {
-        code = 0x7eu;
-    } else if (a < 0x1p-6f) {
-        code = (uint32_t)__builtin_rintf(a * 512.0f);          // subnormal steps of 2^-9
-    } else {
-        uint32_t r = au + 0x7ffffu + ((au >> 20) & 1u);          // RNE at mantissa bit 20
-        code = (r >> 20) - (120u << 3);                          // rebias 127 -> 7
-    }
-    return sign | code;
-}
-
 // ------------------------------------------------------------------ activations
 // GELU, tanh approximation: gelu(x) = x (1 + tanh z) / 2 with z = sqrt(2/pi) (x + 0.044715 x^3).
 // (1 + tanh z) / 2 is the logistic function of 2 z, so gelu(x) = x / (1 + 2^(x (k0 + k1 x^2)))

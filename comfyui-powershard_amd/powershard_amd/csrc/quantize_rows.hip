@@ -203,14 +203,14 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 if constexpr (FP8) {
-                    uint32_t word = 0;
+                    // gfx950's v_cvt_pk_fp8_f32 is the OCP e4m3fn encode with round to nearest
+                    // even (subnormals included); the clamp keeps it off the overflow path
+                    float u[4];
 #pragma unroll
-                    for (int b = 0; b < 4; b++) {
-                        float u = v[rr][c][4 * i + b] * r[rr];
-                        u = __builtin_fminf(__builtin_fmaxf(u, -448.0f), 448.0f);
-                        word |= f32_to_e4m3(u) << (8 * b);
-                    }
-                    packed[i] = word;
+                    for (int b = 0; b < 4; b++)
+                        u[b] = __builtin_fminf(__builtin_fmaxf(v[rr][c][4 * i + b] * r[rr], -448.0f), 448.0f);
+                    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(u[0], u[1], 0, false);
+                    packed[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(u[2], u[3], lo, true);
                 } else {
                     uint32_t cb[4];
 #pragma unroll
