@@ -203,6 +203,17 @@ __device__ __forceinline__ float radix4_lanes(float x)
     return __builtin_fmaf(-2.0f, r, s);
 }
 
+// The same stage with the outputs of the digit reversed: lane d keeps y_{3-d} = S - 2 x_d, its
+// own value, so no third exchange.  The caller stores the lane's elements at digit 3 - d (lane
+// index bits of weight L complemented).
+template <int L>
+__device__ __forceinline__ float radix4_lanes_rev(float x)
+{
+    float t = x + lane_xor<L, 1>(x);
+    float s = t + lane_xor<L, 2>(t);
+    return __builtin_fmaf(-2.0f, x, s);
+}
+
 // ------------------------------------------------------------------ XCD-aware tile order
 // gfx950 dispatches workgroup i to XCD (i % 8).  Re-number so that each XCD receives a
 // contiguous range of logical tiles, then walk tiles in groups of `group_m` tile rows so

@@ -15,9 +15,11 @@
 // chunk per 1024 threads of the row.  Base-4
 // digits 0 and 1 of the element index live inside a thread, digit 2 on lane bits 0-1 (DPP quad
 // permutes), digit 3 on lane bits 2-3 (DPP row mirrors/rotates), digit 4 on lane bits 4-5
-// (cross-lane shuffle; g = 1024 only).  The row's absmax is reduced across the wave with
-// shuffles and across waves through LDS.  HBM-bound: 2 bytes read + 1 byte written per element
-// (+4 bytes per row).
+// (cross-lane shuffle; g = 1024 only).  The lane stages of digits 2 and 3 leave their outputs in
+// reversed digit order (each lane keeps the output its own input enters with -2), so a thread
+// stores its results at the chunk of lane t ^ rev_lanes: same values, one exchange fewer per
+// stage.  The row's absmax is reduced across the wave with DPP and row swaps and across waves
+// through LDS.  2 bytes read + 1 byte written per element (+4 bytes per row).
 #include "psq_common.hpp"
 
 namespace psq {
@@ -91,7 +93,11 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uin
 }
 
 // Unnormalized transform of the 16 values of this thread (in-thread digits) and of the
-// cross-lane digits, for a group size of 4^ROTK.
+// cross-lane digits, for a group size of 4^ROTK.  Digits 2 and 3 (lane bits 0-1 and 2-3) come out
+// reversed (radix4_lanes_rev): the thread's 16 results belong to the chunk of thread t ^ rev_lanes.
+template <int ROTK>
+constexpr int rev_lanes() { return (ROTK >= 3 ? 3 : 0) | (ROTK >= 4 ? 12 : 0); }
+
 template <int ROTK>
 __device__ __forceinline__ void rotate16(float (&v)[16])
 {
@@ -105,11 +111,11 @@ __device__ __forceinline__ void rotate16(float (&v)[16])
     }
     if constexpr (ROTK >= 3) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<1>(v[j]);
+        for (int j = 0; j < 16; j++) v[j] = radix4_lanes_rev<1>(v[j]);
     }
     if constexpr (ROTK >= 4) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<4>(v[j]);
+        for (int j = 0; j < 16; j++) v[j] = radix4_lanes_rev<4>(v[j]);
     }
     if constexpr (ROTK >= 5) {
 #pragma unroll
@@ -218,7 +224,7 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
                     packed[i] = pack_low_bytes(cb[0], cb[1], cb[2], cb[3]);
                 }
             }
-            *(v4i *)(q + (int64_t)row * ldq + (int64_t)(c * T + t) * kElemsPerThread) =
+            *(v4i *)(q + (int64_t)row * ldq + (int64_t)(c * T + (t ^ rev_lanes<ROTK>())) * kElemsPerThread) =
                 v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
         }
     }
@@ -242,7 +248,7 @@ rotate_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int K, void *__r
         float v[16];
         to_f32<DT>(raw, v);
         rotate16<ROTK>(v);
-        const int64_t e0 = (int64_t)row * ldy + (int64_t)(c * T + t) * kElemsPerThread;
+        const int64_t e0 = (int64_t)row * ldy + (int64_t)(c * T + (t ^ rev_lanes<ROTK>())) * kElemsPerThread;
         if constexpr (OUT == PSQ_F32) {
             float *o = (float *)y + e0;
 #pragma unroll
