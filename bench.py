@@ -15,8 +15,8 @@ OpenMP) on a bounded sample of rows of the same workload, on this host's cores.
 
 `extra` carries the other shapes: the int4 (W4A16) text-encoder MLP at M=512 with an M sweep,
 the fp8 QKV projection, the int8 weight-only layer, the Wan-14B FFN with its GELU in the
-up-projection's epilogue against the unfused reference sequence, and the 40-block Wan-14B linear
-stack.
+up-projection's epilogue against the unfused reference sequence, the 8-way token shard's per-GPU
+share (M=4095), and the 40-block Wan-14B linear stack.
 """
 import argparse
 import json
@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--extras", default="", help="comma-separated subset of the extra workloads to run "
-                    "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, wan14b_stack); default all")
+                    "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, shard_m4095, wan14b_stack); default all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample time")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -351,6 +351,42 @@ def extra_ffn(args):
     return res
 
 
+def extra_shard(args):
+    """The per-GPU share of the 8-way token-sharded Wan-14B layer (M_local = ceil(32760 / 8) = 4095):
+    the headline QuantLinear forward and one Wan block of W8A8+ConvRot linears at that M, to set
+    against the single-GPU figures when planning the sharded path (one GPU runs it here)."""
+    import torch
+    M, D, F, cfg = 4095, 5120, 13824, 4
+    opts = {"convrot": True, "convrot_groupsize": 256}
+    from powershard_amd.quant_linear import reuse_quantized_inputs
+    up = quant_layer(D, F, "int8", 1, opts=opts)[0]
+    x = activations(M, D, 1)
+    steps = max(10, args.steps)
+    with torch.no_grad():
+        fwd_ms = untimed_kernel_ms(lambda: up(x), steps, 3)
+    layers = [quant_layer(D, D, "int8", cfg, seed=2000 + i, opts=opts)[0] for i in range(4)]
+    down = quant_layer(F, D, "int8", cfg, seed=2010, opts=opts)[0]
+    xs = activations(M, D, cfg, outlier_scale=50.0, student_t=True)
+    h = activations(M, F, cfg + 100, outlier_scale=50.0, student_t=True)
+    q, k, v, o = layers
+
+    def block():
+        with torch.no_grad():
+            with reuse_quantized_inputs():
+                q(xs); k(xs); v(xs)
+            o(xs); up(xs); down(h)
+    block_ms = untimed_kernel_ms(block, steps, 2)
+    ops_block = 2.0 * M * (4 * D * D + 2 * D * F)
+    res = dict(workload="8-way token shard of Wan-14B at M_local=4095: FFN up forward and one block (W8A8+ConvRot)",
+               up_forward_ms=fwd_ms, up_forward_tops=2.0 * M * D * F / (fwd_ms * 1e-3) / 1e12,
+               block_ms=block_ms, block_tops=ops_block / (block_ms * 1e-3) / 1e12)
+    log(f"[bench] shard M=4095: up forward {fwd_ms:.3f} ms ({res['up_forward_tops']:.0f} TOPS), "
+        f"block {block_ms:.3f} ms ({res['block_tops']:.0f} TOPS)")
+    del layers, up, down, x, xs, h
+    torch.cuda.empty_cache()
+    return res
+
+
 def extra_w8a16(args):
     import torch
     M, K, N, cfg = 1024, 5120, 5120, 0
@@ -416,7 +452,8 @@ def main():
     extra = {}
     if not args.no_extra:
         for name, fn in (("int4_w4a16", extra_int4), ("fp8", extra_fp8), ("w8a16", extra_w8a16),
-                         ("wan_ffn_gelu", extra_ffn), ("wan14b_stack", extra_wan_stack)):
+                         ("wan_ffn_gelu", extra_ffn), ("shard_m4095", extra_shard),
+                         ("wan14b_stack", extra_wan_stack)):
             if args.extras and name not in args.extras.split(","):
                 continue
             try:
