@@ -299,6 +299,9 @@ def reuse_quantized_inputs():
     in-place version of the rows tensor, the same rotation group / format / static scale, and the
     same stream; the cache holds a reference to the rows, so their memory cannot be reused while it
     lives, and it is dropped when the block exits.  Values are those of the uncached path.
+    Inference tensors (torch.inference_mode, as ComfyUI runs) have no version counter, so there an
+    in-place change of the input between two calls inside the block goes unnoticed: wrap only
+    consecutive uses of one unchanged input, as the q, k, v projections are.
     """
     prev = getattr(_shared, "cache", None)
     _shared.cache = {}
@@ -313,7 +316,11 @@ def _quantize_input(rows, fp8, group, input_scale):
     cache = getattr(_shared, "cache", None)
     if cache is None:
         return ops.quantize_rows(rows, fp8=fp8, rot_group=group, static_scale=input_scale)
-    key = (rows.data_ptr(), tuple(rows.shape), tuple(rows.stride()), rows.dtype, rows._version, bool(fp8),
+    try:
+        version = rows._version
+    except RuntimeError:   # inference tensors (torch.inference_mode) carry no version counter
+        version = None
+    key = (rows.data_ptr(), tuple(rows.shape), tuple(rows.stride()), rows.dtype, version, bool(fp8),
            int(group or 0), None if input_scale is None else (input_scale.data_ptr(), input_scale._version),
            torch.cuda.current_stream(rows.device).cuda_stream)
     hit = cache.get(key)

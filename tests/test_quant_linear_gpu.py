@@ -165,6 +165,15 @@ def test_reuse_quantized_inputs(gpu, weight_format, opts):
     for a, b in zip(got, ref):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert torch.equal(got2.view(torch.int16), ref[0].view(torch.int16))
+    # under inference_mode (no version counter) the three calls still share one quantization
+    with torch.inference_mode():
+        xi = heavy_rows(300, K, seed=45).to(gpu)
+        refi = [l(xi) for l in layers]
+        with ops.kernel_timer() as ev, reuse_quantized_inputs():
+            goti = [l(xi) for l in layers]
+        assert len(ev.get(name, [])) == 1
+        for a, b in zip(goti, refi):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     with torch.no_grad():
         assert torch.equal(got3.view(torch.int16), layers[0](x).view(torch.int16))
         assert torch.equal(got4.view(torch.int16), layers[1](x).view(torch.int16))
