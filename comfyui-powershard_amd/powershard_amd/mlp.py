@@ -11,10 +11,16 @@ fp32 GELU, fc2's bf16 cast).  Here fc1's W8A8 / FP8 GEMM applies the GELU to its
 the epilogue and writes the bf16 values fc2's cast would produce, once (QuantLinear.forward_act).
 The reference's memory planner (``mlp_plan`` / ``mlp_budget``, chunk sizing from an allocator
 budget) is not part of this package: ``chunk_tokens`` fixes the chunk size, None = one chunk.
+With ``prepare_budget`` and more than one chunk, Int8Linear layers on their row-tile path
+dequantize their tiles once for all chunks (operations.prepared_linears, as the reference's H3
+chunked MLP does, powershard/fp16_safe.py:126-172).
 """
+import contextlib
+
 import torch
 import torch.nn.functional as F
 
+from .operations import prepared_linears
 from .quant_linear import QuantLinear
 
 __all__ = ["gelu_linear", "chunked_mlp"]
@@ -27,11 +33,12 @@ def gelu_linear(linear, rows):
     return F.gelu(linear(rows).float(), approximate="tanh")
 
 
-def chunked_mlp(fc1, fc2, x, chunk_tokens=None):
+def chunked_mlp(fc1, fc2, x, chunk_tokens=None, prepare_budget=None):
     """fc2(gelu_tanh(fc1(x))) in fp32, computed over chunks of ``chunk_tokens`` token rows.
 
     Follows wan_model.py:589-630: the result is fp32 [..., fc2.out_features]; each chunk's rows
-    are independent, so the chunk size does not change any value.
+    are independent, so the chunk size does not change any value.  ``prepare_budget`` (bytes)
+    bounds the tile cache of ``prepared_linears``; it does not change any value either.
     """
     shape = x.shape
     rows = x.reshape(-1, shape[-1])
@@ -40,9 +47,11 @@ def chunked_mlp(fc1, fc2, x, chunk_tokens=None):
         raise ValueError("chunk_tokens must be positive")
     step = max(n, 1) if chunk_tokens is None else int(chunk_tokens)
     result = torch.empty((n, fc2.out_features), dtype=torch.float32, device=x.device)
-    for a in range(0, n, step):
-        b = min(a + step, n)
-        hidden = gelu_linear(fc1, rows[a:b])
-        result[a:b] = fc2(hidden).float()
-        del hidden
+    prepare = prepare_budget is not None and n > step
+    with prepared_linears((fc1, fc2), prepare_budget) if prepare else contextlib.nullcontext():
+        for a in range(0, n, step):
+            b = min(a + step, n)
+            hidden = gelu_linear(fc1, rows[a:b])
+            result[a:b] = fc2(hidden).float()
+            del hidden
     return result.reshape(shape[:-1] + (fc2.out_features,))

@@ -1,7 +1,7 @@
 """ConvRot int8 helpers and Int8Linear (the ``precision=int8_fp16`` storage).
 
-Mirrors powershard/operations.py:72-155: ``regular_hadamard`` (72-81), ``dequantize_rows``
-(84-93), ``Int8Linear`` (96-132) and ``install_int8`` (135-155).  On a GPU the row dequantization
+Mirrors powershard/operations.py:72-191: ``regular_hadamard`` (72-81), ``dequantize_rows``
+(84-93), ``Int8Linear`` (96-132), ``install_int8`` (135-155) and ``prepared_linears`` (158-191).  On a GPU the row dequantization
 runs the gfx950 kernel (``psq_dequant_i8_rows``: q * s, then the ConvRot inverse by the fast
 transform); on the CPU it is the reference's torch formula.
 
@@ -11,6 +11,7 @@ group (H symmetric, H H^T = I), x W^T = (x H)(q s)^T, so the forward is the acti
 epilogue).  The reference's per-tile dequantize + F.linear remains the path on the CPU, in the fp32
 island and for shapes the kernels do not take.
 """
+from contextlib import contextmanager
 from functools import lru_cache
 
 import torch
@@ -66,10 +67,14 @@ class Int8Linear(nn.Module):
             out = self._native_forward(x, check=tracker is None)
         if out is None:
             out = torch.empty(x.shape[:-1] + (self.out_features,), dtype=x.dtype, device=x.device)
+            prepared = getattr(self, "_ps_prepared", None)
             for a in range(0, self.out_features, self.rows):
                 b = min(a + self.rows, self.out_features)
-                w = dequantize_rows(self.weight[a:b], self.weight_scale[a:b], self.convrot, self.group_size,
-                                    dtype=torch.float32 if safe else torch.float16, check=tracker is None)
+                if prepared is not None and prepared[a // self.rows].dtype == x.dtype:
+                    w = prepared[a // self.rows]
+                else:
+                    w = dequantize_rows(self.weight[a:b], self.weight_scale[a:b], self.convrot, self.group_size,
+                                        dtype=torch.float32 if safe else torch.float16, check=tracker is None)
                 bias = None if self.bias is None else self.bias[a:b].to(x.dtype)
                 out[..., a:b] = F.linear(x, w, bias)
                 del w
@@ -79,6 +84,10 @@ class Int8Linear(nn.Module):
             raise FloatingPointError("NaN/Inf after the INT8 -> FP16 Linear")
         return out
 
+
+    def _tiled(self):
+        """True when the forward dequantizes row tiles (CPU, the fp32 island, the kernels refused)."""
+        return getattr(self, "_ps_safe", False) or self.weight.device.type != "cuda" or not getattr(self, "_ps_native", True)
 
     def _native_forward(self, x, check):
         """fp16 x [..., K] -> fp16 [..., N] on the gfx950 kernels, or None (and the tile path from
@@ -121,3 +130,36 @@ def install_int8(model, quant, rows):
             raise ValueError(f"INT8 expects a Linear/Embedding (got {type(old).__name__}): {name}")
         setattr(parent, leaf, Int8Linear(old, conf, rows))
     return skipped
+
+
+@contextmanager
+def prepared_linears(modules, budget, enabled=True):
+    """Bounded cache of an active MLP's dequantized weight tiles, dropped when the block exits
+    (powershard/operations.py:158-191: the reference keeps it for one MLP over its token chunks).
+
+    Only an Int8Linear on the tile path (the CPU, the fp32 island, shapes the kernels refuse) has
+    tiles to prepare; on the gfx950 kernel path nothing is dequantized, and other modules are left
+    alone.  When ``enabled`` and the tiles' bytes fit ``budget``, each such module's row tiles are
+    dequantized once, in the dtype its forward uses, and reused by every forward inside the block:
+    the values are those of the per-call tiles.  Yields the reference's report keys.
+    """
+    tiled = [m for m in modules if isinstance(m, Int8Linear) and m._tiled()]
+    elem = {id(m): 4 if getattr(m, "_ps_safe", False) else 2 for m in tiled}
+    size = sum(m.in_features * m.out_features * elem[id(m)] for m in tiled)
+    staging = max((4 * m.in_features * min(m.rows, m.out_features) for m in tiled), default=0)
+    use = bool(enabled and tiled and size + staging <= budget)
+    info = dict(prepared_weight_bytes=size if use else 0, preparation_peak_estimate=size + staging if use else 0,
+                preparation="active MLP, reused across token chunks" if use else
+                "per-call tiles; nothing to prepare, preparation budget insufficient or one chunk")
+    try:
+        if use:
+            for m in tiled:
+                dtype = torch.float32 if elem[id(m)] == 4 else torch.float16
+                m._ps_prepared = [dequantize_rows(m.weight[a:a + m.rows], m.weight_scale[a:a + m.rows], m.convrot,
+                                                  m.group_size, dtype=dtype, check=getattr(m, "_ps_tracker", None) is None)
+                                  for a in range(0, m.out_features, m.rows)]
+        yield info
+    finally:
+        for m in modules:
+            if hasattr(m, "_ps_prepared"):
+                del m._ps_prepared

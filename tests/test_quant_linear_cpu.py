@@ -391,3 +391,68 @@ def test_reuse_quantized_inputs_nests_and_restores():
             assert _shared.cache == {}
         assert _shared.cache is outer
     assert _shared.cache is None
+
+
+def _int8linear(K, N, rows, seed, safe=False, group=256):
+    g = torch.Generator().manual_seed(seed)
+    src = nn.Linear(K, N, bias=True, device="meta", dtype=torch.float16)
+    layer = Int8Linear(src, dict(convrot=True, group_size=group), rows=rows).to_empty(device="cpu")
+    layer.weight.data.copy_(torch.randint(-100, 100, (N, K), generator=g, dtype=torch.int8))
+    layer.weight_scale.data.copy_(torch.rand((N, 1), generator=g) * .001)
+    layer.bias.data.copy_((torch.randn(N, generator=g) * 0.1).half())
+    if safe:
+        layer._ps_safe, layer._ps_fp32 = True, False
+    return layer
+
+
+@pytest.mark.parametrize("safe", [False, True])
+def test_prepared_linears_reuse_the_per_call_tiles(safe):
+    """operations.py:158-191: inside the block the tile path reuses tiles dequantized once; the
+    outputs are those of the per-call tiles; the cache is gone after the block, also on an error."""
+    from powershard_amd.operations import prepared_linears
+    fc1, fc2 = _int8linear(512, 40, 16, 1, safe), _int8linear(256, 24, 8, 2, safe)
+    other = nn.Linear(4, 4)
+    x = torch.randn(5, 512).half()
+    h = torch.randn(5, 256).half()
+    ref1, ref2 = fc1(x), fc2(h)
+    with prepared_linears((fc1, fc2, other), budget=1 << 30) as info:
+        assert info["prepared_weight_bytes"] == (512 * 40 + 256 * 24) * (4 if safe else 2)
+        assert len(fc1._ps_prepared) == 3 and len(fc2._ps_prepared) == 3
+        assert torch.equal(fc1(x), ref1) and torch.equal(fc2(h), ref2)
+    assert not hasattr(fc1, "_ps_prepared") and not hasattr(fc2, "_ps_prepared")
+    with prepared_linears((fc1,), budget=100) as info:      # too small: per-call tiles
+        assert info["prepared_weight_bytes"] == 0 and not hasattr(fc1, "_ps_prepared")
+        assert torch.equal(fc1(x), ref1)
+    with pytest.raises(KeyError):
+        with prepared_linears((fc1,), budget=1 << 30, enabled=True):
+            raise KeyError("inside")
+    assert not hasattr(fc1, "_ps_prepared")
+    with prepared_linears((fc1,), budget=1 << 30, enabled=False) as info:
+        assert info["prepared_weight_bytes"] == 0 and not hasattr(fc1, "_ps_prepared")
+
+
+def test_chunked_mlp_prepares_tiles_once_per_mlp(monkeypatch):
+    """tests/test_mlp_policy.py:49-60: over 9 token chunks the row tiles are dequantized once per
+    MLP (8 + 2 tiles), not once per chunk; the values are those of the unprepared loop."""
+    import powershard_amd.operations as ops
+    from powershard_amd import mlp
+    fc1, fc2 = _int8linear(256, 64, 8, 5), _int8linear(64, 16, 8, 6, group=64)
+    x = torch.randn(17, 256)
+    ref = mlp.chunked_mlp(fc1, fc2, x, chunk_tokens=2)
+    count = 0
+    original = ops.dequantize_rows
+
+    def counted(*a, **kw):
+        nonlocal count
+        count += 1
+        return original(*a, **kw)
+    monkeypatch.setattr(ops, "dequantize_rows", counted)
+    out = mlp.chunked_mlp(fc1, fc2, x, chunk_tokens=2, prepare_budget=1 << 30)
+    assert count == 64 // 8 + 16 // 8
+    assert torch.equal(out, ref) and not hasattr(fc1, "_ps_prepared")
+    count = 0
+    mlp.chunked_mlp(fc1, fc2, x, chunk_tokens=2)
+    assert count == 9 * (64 // 8 + 16 // 8)
+    count = 0
+    mlp.chunked_mlp(fc1, fc2, x, prepare_budget=1 << 30)         # one chunk: nothing prepared
+    assert count == 64 // 8 + 16 // 8
