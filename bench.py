@@ -15,8 +15,9 @@ OpenMP) on a bounded sample of rows of the same workload, on this host's cores.
 
 `extra` carries the other shapes: the int4 (W4A16) text-encoder MLP at M=512 with an M sweep,
 the fp8 QKV projection, the int8 weight-only layer, the Wan-14B FFN with its GELU in the
-up-projection's epilogue against the unfused reference sequence, the 8-way token shard's per-GPU
-share (M=4095), and the 40-block Wan-14B linear stack.
+up-projection's epilogue against the unfused reference sequence, the MiniMax-H3 MLP with its SiLU
+gate in fc1's epilogue (fp16, M=8192) against its reference sequence, the 8-way token shard's
+per-GPU share (M=4095), and the 40-block Wan-14B linear stack.
 """
 import argparse
 import json
@@ -77,18 +78,20 @@ def activations(M, K, cfg, outlier_scale=20.0, student_t=False, dev="cuda"):
     return x.to(torch.bfloat16)
 
 
-def quant_layer(K, N, weight_format, cfg, seed=None, opts=None, dev="cuda"):
-    """A QuantLinear installed and filled through the package's own install/pack path."""
+def quant_layer(K, N, weight_format, cfg, seed=None, opts=None, dev="cuda", dtype=None):
+    """A QuantLinear installed and filled through the package's own install/pack path (compute
+    dtype bf16 unless given)."""
     import torch
     from torch import nn
     from powershard_amd.quant_linear import install_quant_linears, quantized_from_float, pack
     g = gen(1000 + cfg if seed is None else seed)
     w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-    b = (torch.randn(N, generator=gen(3000 + cfg), device=dev) * 0.01).to(torch.bfloat16)
+    dtype = dtype or torch.bfloat16
+    b = (torch.randn(N, generator=gen(3000 + cfg), device=dev) * 0.01).to(dtype)
     with torch.device("meta"):
-        net = nn.Sequential(nn.Linear(K, N, dtype=torch.bfloat16))
+        net = nn.Sequential(nn.Linear(K, N, dtype=dtype))
     tensors = {"0.weight": {"key": "0.weight", "dtype": "BF16", "shape": [N, K]}}
-    install_quant_linears(net, tensors, weight_format, "native", None, torch.bfloat16, torch.device(dev),
+    install_quant_linears(net, tensors, weight_format, "native", None, dtype, torch.device(dev),
                           quant_options=opts)
     layer = net[0]
     qt = quantized_from_float(w, layer._ps_qplan.fmt, **(opts or {}))
@@ -351,6 +354,43 @@ def extra_ffn(args):
     return res
 
 
+def extra_h3_mlp(args):
+    """MiniMax-H3 MLP (powershard/fp16_safe.py:126-172; fc1 28672x5376, fc2 5376x14336 as in the
+    reference's int8-ConvRot checkpoint headers) at M=8192 synthetic tokens, fp16 compute
+    (h3_quant.py:101-105), W8A8+ConvRot: the reference sequence gate, up = fc1(x).chunk(2, -1);
+    fc2(F.silu(gate.float()) * up.float()) against the gate in fc1's epilogue."""
+    import torch
+    import torch.nn.functional as Fn
+    M, D, F, cfg = 8192, 5376, 14336, 5
+    opts = {"convrot": True, "convrot_groupsize": 256}
+    fc1 = quant_layer(D, 2 * F, "int8", cfg, seed=5000, opts=opts, dtype=torch.float16)[0]
+    fc2 = quant_layer(F, D, "int8", cfg, seed=5001, opts=opts, dtype=torch.float16)[0]
+    # N(0,1) with 1% of channels x20: fc1's outputs stay well inside fp16 (heavier tails overflow
+    # the fp16 hidden of the reference sequence itself)
+    x = activations(M, D, cfg).to(torch.float16)
+    steps = max(3, min(args.steps, 10))
+
+    def unfused():
+        gate, up = fc1(x).chunk(2, -1)
+        return fc2(Fn.silu(gate.float()) * up.float())
+    res = {"workload": "MiniMax-H3 MLP fc1 5376->2x14336, SiLU gate, fc2 14336->5376, W8A8+ConvRot, fp16, M=8192"}
+    with torch.no_grad():
+        res["unfused_ms"] = untimed_kernel_ms(unfused, steps, 1)
+        res["fused_ms"] = untimed_kernel_ms(lambda: fc2(fc1.forward_act(x, "silu_gate")), steps, 1)
+        res["fc1_ms"] = untimed_kernel_ms(lambda: fc1(x), steps, 1)
+        res["fc1_gate_ms"] = untimed_kernel_ms(lambda: fc1.forward_act(x, "silu_gate"), steps, 1)
+        ref = unfused().float()
+        got = fc2(fc1.forward_act(x, "silu_gate")).float()
+        if not (torch.isfinite(ref).all() and torch.isfinite(got).all()):
+            raise RuntimeError("h3 mlp: non-finite outputs")
+        res["max_err_over_rms"] = ((got - ref).abs().max() / ref.pow(2).mean().sqrt()).item()
+    log(f"[bench] h3 mlp: unfused {res['unfused_ms']:.3f} ms, fused {res['fused_ms']:.3f} ms; fc1 GEMM "
+        f"{res['fc1_ms']:.3f} ms, with the gate {res['fc1_gate_ms']:.3f} ms; max err/rms {res['max_err_over_rms']:.2e}")
+    del fc1, fc2, x
+    torch.cuda.empty_cache()
+    return res
+
+
 def extra_shard(args):
     """The per-GPU share of the 8-way token-sharded Wan-14B layer (M_local = ceil(32760 / 8) = 4095):
     the headline QuantLinear forward and one Wan block of W8A8+ConvRot linears at that M, to set
@@ -452,7 +492,8 @@ def main():
     extra = {}
     if not args.no_extra:
         for name, fn in (("int4_w4a16", extra_int4), ("fp8", extra_fp8), ("w8a16", extra_w8a16),
-                         ("wan_ffn_gelu", extra_ffn), ("shard_m4095", extra_shard),
+                         ("wan_ffn_gelu", extra_ffn), ("h3_mlp_silu_gate", extra_h3_mlp),
+                         ("shard_m4095", extra_shard),
                          ("wan14b_stack", extra_wan_stack)):
             if args.extras and name not in args.extras.split(","):
                 continue

@@ -8,6 +8,10 @@
 // With an epilogue activation (GELU, tanh form; the Wan FFN's F.gelu(fc1(x).float(),
 // approximate="tanh"), powershard/wan_model.py:626) the store writes round_out(act(round_out(y))):
 // the GELU of the rounded linear output, rounded to the dtype the next layer casts it to.
+// With the SiLU gate (the H3 MLP's silu(gate) * up, powershard/fp16_safe.py:165-167) the weight's
+// N rows are N / 2 gate rows followed by N / 2 up rows; a tile reads its W rows as 64 gate rows
+// and their 64 up rows per wave-column block, so each gate value meets its up value in the same
+// lane and register, and the store writes round_out(silu(round_out(g)) round_out(u)) to [M, N / 2].
 //
 // Tiling (MI355X-first): a persistent grid of one workgroup per CU walks 256 x 256 output tiles;
 // a workgroup is 4 waves, one per SIMD (2 x 2, each wave 128 x 128 = 4 x 4 MFMA tiles of 32 x 32,
@@ -82,7 +86,7 @@ __device__ __forceinline__ uint32_t pack2(float a, float b)
 template <int OUT, int ACT>
 __device__ __forceinline__ float act1(float v)
 {
-    if constexpr (ACT == ACT_NONE || OUT == OUT_I32) return v;
+    if constexpr (ACT != ACT_GELU_TANH || OUT == OUT_I32) return v;
     else if constexpr (OUT == OUT_F32) return gelu_tanh(v);
     else {
         constexpr int DT = OUT == OUT_BF16 ? PSQ_BF16 : PSQ_F16;
@@ -94,7 +98,7 @@ __device__ __forceinline__ float act1(float v)
 template <int OUT, int ACT>
 __device__ __forceinline__ uint32_t pack2a(float a, float b)
 {
-    if constexpr (ACT == ACT_NONE) {
+    if constexpr (ACT != ACT_GELU_TANH) {
         return pack2<OUT>(a, b);
     } else {
         const uint32_t p = pack2<OUT>(a, b);
@@ -108,6 +112,37 @@ __device__ __forceinline__ uint32_t pack2a(float a, float b)
         }
         return pack2<OUT>(gelu_tanh(ra), gelu_tanh(rb));
     }
+}
+
+// The gate: silu(g) u on the outputs rounded to their dtype (fp32 outputs: unrounded).
+template <int OUT>
+__device__ __forceinline__ float gate1(float g, float u)
+{
+    if constexpr (OUT == OUT_F32) return silu(g) * u;
+    else {
+        constexpr int DT = OUT == OUT_BF16 ? PSQ_BF16 : PSQ_F16;
+        return silu(half_to_f32<DT>(f32_to_half<DT>(g))) * half_to_f32<DT>(f32_to_half<DT>(u));
+    }
+}
+
+// Two gated outputs packed (as gate1): the inner roundings are the same packed conversion.
+template <int OUT>
+__device__ __forceinline__ uint32_t pack2g(float g0, float u0, float g1, float u1)
+{
+    const uint32_t pg = pack2<OUT>(g0, g1), pu = pack2<OUT>(u0, u1);
+    float rg0, rg1, ru0, ru1;
+    if constexpr (OUT == OUT_BF16) {
+        rg0 = __uint_as_float(pg << 16);
+        rg1 = __uint_as_float(pg & 0xffff0000u);
+        ru0 = __uint_as_float(pu << 16);
+        ru1 = __uint_as_float(pu & 0xffff0000u);
+    } else {
+        rg0 = f16_to_f32(pg & 0xffffu);
+        rg1 = f16_to_f32(pg >> 16);
+        ru0 = f16_to_f32(pu & 0xffffu);
+        ru1 = f16_to_f32(pu >> 16);
+    }
+    return pack2<OUT>(silu(rg0) * ru0, silu(rg1) * ru1);
 }
 
 // One output element (the slow path of partial tiles and unaligned outputs).
@@ -230,6 +265,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     constexpr int KS = BK / Frag<FP8>::KSTEP;      // k-steps per stage: 4 (int8), 2 (fp8)
     constexpr bool SCALED = OUT != OUT_I32;
     constexpr int LATE = late_loads<FP8>();         // loads of stage kt + 2 behind the last k-step
+    constexpr bool GATED = ACT == ACT_SILU_GATE;
 
     // wave-uniform values in scalar registers: the LDS destination of every global->LDS load (M0)
     // is then computed without a VALU -> SGPR round trip
@@ -252,6 +288,10 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     // registers) plus a per-lane 32-bit offset -- the scalar-base form of global_load_lds, so a
     // load costs no 64-bit vector address arithmetic.  Rows past M (N) are clamped to the last
     // row; the tile's stores skip them.
+    // With the gate, column n of the GEMM (W row) is stored row wrow(n): within each 128-column
+    // block, 64 gate rows and then the same 64 columns' up rows, N / 2 rows further on.
+    const int half_n = N >> 1;
+    auto wrow = [&](int n) { return GATED ? ((n & 127) >> 6) * half_n + ((n >> 7) << 6) + (n & 63) : n; };
     const uint8_t *ba = nullptr, *bw = nullptr;       // current tile
     const uint8_t *nba = nullptr, *nbw = nullptr;     // next tile
     uint32_t oa[LOADS], ow[LOADS];                    // current tile's lane offsets
@@ -261,19 +301,20 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         int m0, n0;
         tile_coords(tv, nbm, nbn, m0, n0);
         pa = A + (int64_t)m0 * lda;
-        pw = W + (int64_t)n0 * ldw;
+        pw = GATED ? W : W + (int64_t)n0 * ldw;   // gated: offsets from the weight's first row
 #pragma unroll
         for (int j = 0; j < LOADS; j++) {
             const int b = j * (NTHREADS / 64) + wave;
             const int r = 8 * b + (lane >> 3);
             const int c = (lane & 7) ^ chunk_xor(r);
             qa[j] = (uint32_t)(min(r, M - 1 - m0) * lda + c * 16);
-            qw[j] = (uint32_t)(min(r, N - 1 - n0) * ldw + c * 16);
+            if constexpr (GATED) qw[j] = (uint32_t)wrow(n0 + min(r, N - 1 - n0)) * (uint32_t)ldw + (uint32_t)(c * 16);
+            else qw[j] = (uint32_t)(min(r, N - 1 - n0) * ldw + c * 16);
         }
         if constexpr (SCALED) {
             // the tile's row scales, column scales and bias words: 64 entries of each per wave
             lds_ptr dst = (lds_ptr)(scale_lds + buf * SCALE_WORDS + 64 * wave);
-            const int m = min(m0 + 64 * wave + lane, M - 1), n = min(n0 + 64 * wave + lane, N - 1);
+            const int m = min(m0 + 64 * wave + lane, M - 1), n = wrow(min(n0 + 64 * wave + lane, N - 1));
             __builtin_amdgcn_global_load_lds((glb_ptr)(ep.a_scale + m), dst, 4, 0, 0);
             __builtin_amdgcn_global_load_lds((glb_ptr)(ep.w_scale + (ep.w_per_row ? n : 0)), dst + 4 * BM, 4, 0, 0);
             if (ep.bias) {
@@ -430,6 +471,102 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             const float a = FP8 ? __int_as_float(x) : (float)x;
             return __builtin_fmaf(a, as[i] * w, b);
         };
+        if constexpr (GATED) {
+            // The wave's 128 GEMM columns are 64 gate columns (acc[i][0..1]) and their up columns
+            // (acc[i][2..3]): register 4 g + c of acc[i][jj] and of acc[i][jj + 2] is output column
+            // ob + 32 jj + 8 g + 4 (l >> 5) + c, ob = (n0 + 128 wn) / 2.  N is a multiple of 128,
+            // so a wave's block is whole or past N.
+            const int nb = n0 + wn * WAVE_N;
+            if (nb >= N) return;
+            const int ob = nb >> 1;
+            if constexpr (PSQ_Q8_STAGED && (OUT == OUT_BF16 || OUT == OUT_F16)) {
+                if (ep.vec) {
+                    // one 32 x 64 block per row block i, staged through LDS as in the ungated
+                    // epilogue below: whole-line stores
+                    uint8_t *const eb = smem + kEpiOffset + wave * EPI_WAVE_BYTES;
+                    const int h = lane >> 5;
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+#pragma unroll
+                        for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+                            for (int pr = 0; pr < 2; pr++) {
+                                const int nc = 32 * jj + 16 * pr;
+                                float wg[2][4], bg[2][4], wu[2][4], bu[2][4];
+                                operands(nc, wg[0], bg[0]);
+                                operands(nc + 8, wg[1], bg[1]);
+                                operands(nc + 64, wu[0], bu[0]);
+                                operands(nc + 72, wu[1], bu[1]);
+                                uint32_t x[2], y[2];
+#pragma unroll
+                                for (int hh = 0; hh < 2; hh++) {
+                                    uint32_t *o = hh == 0 ? x : y;
+                                    const int r = 8 * pr + 4 * hh;
+#pragma unroll
+                                    for (int e = 0; e < 2; e++)
+                                        o[e] = pack2g<OUT>(value(i, jj, r + 2 * e, wg[hh][2 * e], bg[hh][2 * e]),
+                                                           value(i, jj + 2, r + 2 * e, wu[hh][2 * e], bu[hh][2 * e]),
+                                                           value(i, jj, r + 2 * e + 1, wg[hh][2 * e + 1], bg[hh][2 * e + 1]),
+                                                           value(i, jj + 2, r + 2 * e + 1, wu[hh][2 * e + 1], bu[hh][2 * e + 1]));
+                                }
+                                uint32_t lo[2], hi[2];
+#pragma unroll
+                                for (int d = 0; d < 2; d++) {
+                                    const auto sw = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
+                                    lo[d] = sw[0];
+                                    hi[d] = sw[1];
+                                }
+                                const int ch = 4 * jj + 2 * pr + h;
+                                *(v4i *)(eb + frow * 128 + ((ch ^ chunk_xor(frow)) << 4)) =
+                                    v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                                __builtin_amdgcn_sched_barrier(0);
+                            }
+                        v4i val[4];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int row = 8 * q + (lane >> 3), ch = lane & 7;
+                            val[q] = *(const v4i *)(eb + row * 128 + ((ch ^ chunk_xor(row)) << 4));
+                        }
+                        const int mb = m0 + wm * WAVE_M + 32 * i;
+                        const int64_t ubase = ((int64_t)mb * ep.ldy + ob) * 2;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int row = 8 * q + (lane >> 3);
+                            if (mb + row < M) {
+                                const uint32_t loff = (uint32_t)((row * ep.ldy + 8 * (lane & 7)) * 2);
+                                v4i *dst = (v4i *)((uint8_t *)ep.y + ubase + loff);
+                                if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val[q], dst);
+                                else *dst = val[q];
+                            }
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    return;
+                }
+            }
+            // fp32 outputs and unaligned rows: element stores
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int nc = 32 * jj + 8 * g;
+                    float wg[4], bg[4], wu[4], bu[4];
+                    operands(nc, wg, bg);
+                    operands(nc + 64, wu, bu);
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        if (!live[i]) continue;
+                        const int m = m0 + wm * WAVE_M + 32 * i + frow;
+                        void *p = (uint8_t *)ep.y + ((int64_t)m * ep.ldy + ob + nc + 4 * (lane >> 5)) * esz;
+#pragma unroll
+                        for (int c = 0; c < 4; c++)
+                            store1<OUT>(p, c, gate1<OUT>(value(i, jj, 4 * g + c, wg[c], bg[c]),
+                                                         value(i, jj + 2, 4 * g + c, wu[c], bu[c])));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            return;
+        }
         if constexpr (PSQ_Q8_STAGED && (OUT == OUT_BF16 || OUT == OUT_F16)) {
             if (ep.vec && n0 + BN <= N) {
                 // Full-width tile, aligned rows, 16-bit outputs: the wave's 128 x 128 block leaves
@@ -803,6 +940,13 @@ template <bool FP8>
 int launch(int out, int act, const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N,
            int64_t K, const Epi &ep, hipStream_t st, const char *name)
 {
+    if (act == ACT_SILU_GATE) {
+        switch (out) {
+        case OUT_BF16: return launch_one<FP8, OUT_BF16, ACT_SILU_GATE>(a, lda, w, ldw, M, N, K, ep, st, name);
+        case OUT_F16: return launch_one<FP8, OUT_F16, ACT_SILU_GATE>(a, lda, w, ldw, M, N, K, ep, st, name);
+        default: return launch_one<FP8, OUT_F32, ACT_SILU_GATE>(a, lda, w, ldw, M, N, K, ep, st, name);
+        }
+    }
     if (act == ACT_GELU_TANH) {
         switch (out) {
         case OUT_BF16: return launch_one<FP8, OUT_BF16, ACT_GELU_TANH>(a, lda, w, ldw, M, N, K, ep, st, name);
@@ -843,6 +987,23 @@ int check_shapes(const char *name, const void *a, int64_t lda, const void *w, in
     return PSQ_OK;
 }
 
+// Activation codes, and the gate's shape rules: N = 2 H rows with H a multiple of 64, an output of
+// H columns, and every W row offset (row ldw, 32-bit lane offsets from the weight's first row)
+// plus the k offset below 2^32.
+int check_act(const char *name, int activation, int64_t N, int64_t ldw, int64_t K, int64_t ldy)
+{
+    if (activation != ACT_NONE && activation != ACT_GELU_TANH && activation != ACT_SILU_GATE)
+        return set_error(PSQ_E_ARG, "%s: bad activation %d", name, activation);
+    if (activation == ACT_SILU_GATE) {
+        if (N % 128) return set_error(PSQ_E_SHAPE, "%s: the SiLU gate needs N a multiple of 128, got %lld", name, (long long)N);
+        if (N * ldw + K >= (1LL << 32)) return set_error(PSQ_E_SHAPE, "%s: the SiLU gate needs N ldw + K < 2^32", name);
+        if (ldy < N / 2) return set_error(PSQ_E_SHAPE, "%s: ldy < N / 2", name);
+    } else if (ldy < N) {
+        return set_error(PSQ_E_SHAPE, "%s: ldy < N", name);
+    }
+    return PSQ_OK;
+}
+
 }  // namespace
 }  // namespace psq
 
@@ -854,11 +1015,10 @@ int psq_gemm_i8_act(const int8_t *a, int64_t lda, const float *a_scale, const in
 {
     using namespace psq;
     if (int e = check_shapes("gemm_i8", a, lda, w, ldw, M, N, K)) return e;
-    if (activation != ACT_NONE && activation != ACT_GELU_TANH) return set_error(PSQ_E_ARG, "gemm_i8: bad activation");
+    if (int e = check_act("gemm_i8", activation, N, ldw, K, ldy)) return e;
     if (M == 0 || N == 0) return PSQ_OK;
     if (!a_scale || !w_scale || !y) return set_error(PSQ_E_ARG, "gemm_i8: null scale or output");
     if (!valid_dtype(y_dtype) || (bias && !valid_dtype(bias_dtype))) return set_error(PSQ_E_ARG, "gemm_i8: bad dtype");
-    if (ldy < N) return set_error(PSQ_E_SHAPE, "gemm_i8: ldy < N");
     if (int e = require_device()) return e;
     Epi ep{a_scale, w_scale, 1, bias, bias_dtype, y, ldy, vec_ok(y, ldy, y_dtype == PSQ_F32 ? 4 : 2)};
     return launch<false>(y_dtype, activation, (const uint8_t *)a, lda, (const uint8_t *)w, ldw, M, N, K, ep,
@@ -893,11 +1053,10 @@ int psq_gemm_fp8_act(const uint8_t *a, int64_t lda, const float *a_scale, const 
 {
     using namespace psq;
     if (int e = check_shapes("gemm_fp8", a, lda, w, ldw, M, N, K)) return e;
-    if (activation != ACT_NONE && activation != ACT_GELU_TANH) return set_error(PSQ_E_ARG, "gemm_fp8: bad activation");
+    if (int e = check_act("gemm_fp8", activation, N, ldw, K, ldy)) return e;
     if (M == 0 || N == 0) return PSQ_OK;
     if (!a_scale || !w_scale || !y) return set_error(PSQ_E_ARG, "gemm_fp8: null scale or output");
     if (!valid_dtype(y_dtype) || (bias && !valid_dtype(bias_dtype))) return set_error(PSQ_E_ARG, "gemm_fp8: bad dtype");
-    if (ldy < N) return set_error(PSQ_E_SHAPE, "gemm_fp8: ldy < N");
     if (int e = require_device()) return e;
     Epi ep{a_scale, w_scale, w_scale_per_row ? 1 : 0, bias, bias_dtype, y, ldy, vec_ok(y, ldy, y_dtype == PSQ_F32 ? 4 : 2)};
     return launch<true>(y_dtype, activation, a, lda, w, ldw, M, N, K, ep, (hipStream_t)stream, "gemm_fp8");

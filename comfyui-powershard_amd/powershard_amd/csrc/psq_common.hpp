@@ -125,7 +125,15 @@ __device__ __forceinline__ float gelu_tanh(float x)
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(w));
 }
 
-enum { ACT_NONE = PSQ_ACT_NONE, ACT_GELU_TANH = PSQ_ACT_GELU_TANH };
+// silu(x) = x / (1 + e^-x) = x / (1 + 2^(-x log2 e)); exp2 overflows to +inf for x < -88.7 and the
+// result is then -0 (|silu| < 1e-36 there).
+__device__ __forceinline__ float silu(float x)
+{
+    constexpr float k = (float)(-1.44269504088896340736);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * k));
+}
+
+enum { ACT_NONE = PSQ_ACT_NONE, ACT_GELU_TANH = PSQ_ACT_GELU_TANH, ACT_SILU_GATE = PSQ_ACT_SILU_GATE };
 
 // ------------------------------------------------------------------ stores
 // Store one fp32 value as element i of an output of dtype dt.

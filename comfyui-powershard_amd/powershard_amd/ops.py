@@ -124,7 +124,7 @@ def rotate_rows(x, rot_group, out_dtype=None):
 
 # ----------------------------------------------------------------------- GEMMs
 # epilogue activations of the W8A8 / FP8 GEMMs (enum psq_activation)
-ACTIVATIONS = {None: 0, "none": 0, "gelu_tanh": 1}
+ACTIVATIONS = {None: 0, "none": 0, "gelu_tanh": 1, "silu_gate": 2}
 
 
 def _act(activation):
@@ -134,11 +134,23 @@ def _act(activation):
         raise ValueError(f"unknown epilogue activation {activation!r}") from None
 
 
+def _out_cols(N, act, name):
+    """Output columns: N, or N / 2 for the SiLU gate (gate rows, then up rows)."""
+    if act != ACTIVATIONS["silu_gate"]:
+        return N
+    if N % 128:
+        raise ValueError(f"{name}: the SiLU gate needs N (gate + up rows) a multiple of 128, got {N}")
+    return N // 2
+
+
 def gemm_i8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activation=None):
     """y = round(fmaf(a @ w.T (int32), a_scale[m] * w_scale[n], bias[n])): [M, N] out_dtype.
 
     activation "gelu_tanh": y = round(gelu_tanh(round(...))) -- the GELU of the rounded output,
     rounded again (the Wan FFN's F.gelu(fc1(x).float(), approximate="tanh") then fc2's cast).
+    activation "silu_gate": w holds N / 2 gate rows then N / 2 up rows (N a multiple of 128);
+    y[m, j] = round(silu(round(g)) * round(u)) is [M, N / 2], g and u the linear outputs of
+    columns j and N / 2 + j (the H3 MLP's F.silu(gate.float()) * up.float(), then fc2's cast).
     """
     _need_gpu(a, a_scale, w, w_scale)
     a, w = _rows2d(a), _rows2d(w)
@@ -153,11 +165,11 @@ def gemm_i8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activat
     if a_scale.numel() != M or w_scale.numel() != N:
         raise ValueError("gemm_i8: scale sizes do not match M / N")
     bias, bdt = _bias(bias, N, a.device)
-    y = torch.empty(M, N, dtype=out_dtype, device=a.device)
     act = _act(activation)
+    y = torch.empty(M, _out_cols(N, act, "gemm_i8"), dtype=out_dtype, device=a.device)
     if act:
         _launch("gemm_i8", _native.lib().psq_gemm_i8_act, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale),
-                _p(bias), bdt, act, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
+                _p(bias), bdt, act, _p(y), _dt(y, "out"), y.shape[1], M, N, K, _stream(a))
     else:
         _launch("gemm_i8", _native.lib().psq_gemm_i8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0), _p(w_scale),
                 _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
@@ -194,11 +206,12 @@ def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activa
     if a_scale.numel() != M or w_scale.numel() not in (1, N):
         raise ValueError("gemm_fp8: scale sizes do not match")
     bias, bdt = _bias(bias, N, a.device)
-    y = torch.empty(M, N, dtype=out_dtype, device=a.device)
     act = _act(activation)
+    y = torch.empty(M, _out_cols(N, act, "gemm_fp8"), dtype=out_dtype, device=a.device)
     if act:
         _launch("gemm_fp8", _native.lib().psq_gemm_fp8_act, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0),
-                _p(w_scale), int(w_scale.numel() > 1), _p(bias), bdt, act, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
+                _p(w_scale), int(w_scale.numel() > 1), _p(bias), bdt, act, _p(y), _dt(y, "out"), y.shape[1], M, N, K,
+                _stream(a))
     else:
         _launch("gemm_fp8", _native.lib().psq_gemm_fp8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0),
                 _p(w_scale), int(w_scale.numel() > 1), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))

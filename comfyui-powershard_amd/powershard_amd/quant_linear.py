@@ -231,16 +231,21 @@ class QuantLinear(nn.Module):
         return self._forward(x, None)
 
     def forward_act(self, x, activation="gelu_tanh"):
-        """gelu_tanh(self(x)) with the activation fused into the native GEMM's epilogue.
+        """act(self(x)) with the activation fused into the native GEMM's epilogue.
 
-        The reference applies it outside the linear, F.gelu(fc1(rows).float(),
-        approximate="tanh") (powershard/wan_model.py:626), and the next QuantLinear casts the fp32
-        result to its compute dtype first (quant_linear.py:197).  On the native W8A8 / FP8 path the
-        result comes back in the compute dtype: the values that cast gives, without the fp32
-        intermediate.  Elsewhere it is the reference's fp32 F.gelu of the forward's output.
+        "gelu_tanh": the reference applies it outside the linear, F.gelu(fc1(rows).float(),
+        approximate="tanh") (powershard/wan_model.py:626).  "silu_gate": gate, up =
+        fc1(rows).chunk(2, -1); F.silu(gate.float()) * up.float() (powershard/fp16_safe.py:165-167),
+        [..., out_features / 2].  The next QuantLinear casts the fp32 result to its compute dtype
+        first (quant_linear.py:197).  On the native W8A8 / FP8 path the result comes back in the
+        compute dtype: the values that cast gives, without the fp32 intermediate (the gate fused for
+        out_features a multiple of 128).  Elsewhere it is the reference's fp32 expression on the
+        forward's output.
         """
-        if activation != "gelu_tanh":
+        if activation not in ("gelu_tanh", "silu_gate"):
             raise ValueError(f"unsupported activation {activation!r}")
+        if activation == "silu_gate" and self.out_features % 2:
+            raise ValueError(f"silu_gate needs an even number of output features, got {self.out_features}")
         return self._forward(x, activation)
 
     def _forward(self, x, activation):
@@ -261,9 +266,11 @@ class QuantLinear(nn.Module):
         out = None
         fused = False   # activation applied by native_linear
         if self._ps_native and not safe and not self._ps_full_precision:
+            # the fused gate pairs 64-column blocks: other widths take the gate as a separate pass
+            native_act = None if activation == "silu_gate" and self.out_features % 128 else activation
             try:
-                out = native_linear(rows, qt, bias, plan.fmt, extras.get("input_scale"), activation)
-                fused = activation is not None
+                out = native_linear(rows, qt, bias, plan.fmt, extras.get("input_scale"), native_act)
+                fused = native_act is not None
             except torch.cuda.OutOfMemoryError:
                 raise
             except (NotImplementedError, RuntimeError, TypeError, ValueError) as error:
@@ -275,8 +282,8 @@ class QuantLinear(nn.Module):
         elif out is None:
             out = F.linear(rows, qt.dequantize().to(dtype), bias)
         if activation is not None and not fused:
-            out = F.gelu(out.float(), approximate="tanh")
-        out = out.reshape(shape[:-1] + (self.out_features,))
+            out = apply_activation(out, activation)
+        out = out.reshape(shape[:-1] + (out.shape[-1],))
         if self._ps_follow_input and x.is_floating_point() and out.dtype != x.dtype:
             out = out.to(x.dtype)  # text encoder: the FP32 graph is not narrowed to bf16 by the native kernel
         tracker = getattr(self, "_ps_tracker", None)
@@ -331,11 +338,24 @@ def _quantize_input(rows, fp8, group, input_scale):
     return qx, sx
 
 
+def apply_activation(out, activation):
+    """The reference's fp32 activation of a linear output: F.gelu(out.float(), approximate="tanh")
+    (wan_model.py:626), or for "silu_gate" F.silu(gate.float()) * up.float() over
+    out.chunk(2, -1) (fp16_safe.py:165-167)."""
+    if activation == "gelu_tanh":
+        return F.gelu(out.float(), approximate="tanh")
+    if activation == "silu_gate":
+        gate, up = out.chunk(2, -1)
+        return F.silu(gate.float()) * up.float()
+    raise ValueError(f"unsupported activation {activation!r}")
+
+
 def native_linear(rows, qt, bias, fmt, input_scale=None, activation=None):
     """The native GEMM of one format on the gfx950 kernels (replaces F.linear(QuantizedTensor)).
 
     rows [M, K] in the compute dtype on the GPU; returns [M, N] in rows.dtype.  activation
-    "gelu_tanh" returns gelu(y) rounded to rows.dtype, fused into the W8A8 / FP8 epilogues.
+    "gelu_tanh" returns gelu(y) rounded to rows.dtype, "silu_gate" silu(gate) * up over the two
+    halves of y ([M, N / 2], N a multiple of 128), fused into the W8A8 / FP8 epilogues.
     """
     from . import ops
     if rows.device.type != "cuda":
@@ -351,7 +371,7 @@ def native_linear(rows, qt, bias, fmt, input_scale=None, activation=None):
     if layout is qtm.UInt4GroupLayout:
         out = ops.gemm_w4a16(rows, qt._qdata, p.scale, p.zero, p.group_size, bias, out_dtype=rows.dtype)
         if activation is not None:   # weight-only GEMM: the activation stays a separate pass
-            out = F.gelu(out.float(), approximate="tanh").to(rows.dtype)
+            out = apply_activation(out, activation).to(rows.dtype)
         return out
     raise NotImplementedError(f"no native kernel for {fmt}")
 

@@ -112,7 +112,8 @@ PSQ_API int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, co
 /* GEMM epilogue activations (the *_act entry points). */
 enum psq_activation {
     PSQ_ACT_NONE = 0,
-    PSQ_ACT_GELU_TANH = 1   /* gelu(v) = v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))) / 2 */
+    PSQ_ACT_GELU_TANH = 1,  /* gelu(v) = v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))) / 2 */
+    PSQ_ACT_SILU_GATE = 2   /* h[j] = silu(v[j]) v[H + j], H = N / 2; y is [M, H] */
 };
 
 /* W8A8 / FP8 GEMM with an activation fused into the epilogue:
@@ -126,7 +127,14 @@ enum psq_activation {
  * exact function, and of torch's fp32 F.gelu up to 1e-6 absolute (the fp32 tanh form loses
  * relative precision below v = -3); below v = -9.6 (|gelu| < 1e-37) they are -0.  Arguments as in
  * psq_gemm_i8 / psq_gemm_fp8; y_dtype bf16, f16 or f32 (f32: no inner rounding).
- * activation PSQ_ACT_NONE gives exactly psq_gemm_i8 / psq_gemm_fp8. */
+ * activation PSQ_ACT_NONE gives exactly psq_gemm_i8 / psq_gemm_fp8.
+ * PSQ_ACT_SILU_GATE is the H3 MLP's gate (powershard/fp16_safe.py:165-167:
+ * gate, up = fc1(rows).chunk(2, -1); F.silu(gate.float()) * up.float()): the weight's N rows are
+ * the gate rows, then the up rows, N a multiple of 128 and N ldw + K < 2^32; y is [M, N / 2]
+ * (ldy >= N / 2) with y[m][j] = round_out(silu(g) u), g and u the rounded linear outputs of
+ * columns j and N / 2 + j, silu(g) = g / (1 + exp(-g)) in fp32 (-0 for g < -88.7, where
+ * |silu| < 1e-36).  The pairs meet in registers: a tile's W rows are read as 64 gate rows
+ * followed by their 64 up rows, so the N x K weight is used as stored. */
 PSQ_API int psq_gemm_i8_act(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w,
                     int64_t ldw, const float *w_scale, const void *bias, int bias_dtype, int activation,
                     void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream);

@@ -99,3 +99,42 @@ def test_chunked_mlp_with_quant_linears_on_cpu():
     x = torch.randn(37, 128, generator=seeded(10)).to(torch.bfloat16)
     ref = fc2(F.gelu(fc1(x).float(), approximate="tanh")).float()
     assert torch.equal(mlp.chunked_mlp(fc1, fc2, x, chunk_tokens=16), ref)
+
+
+def test_silu_logistic_form_is_torch_silu():
+    """The epilogue's silu(g) = g / (1 + 2^(-g log2 e)) is torch's F.silu (fp16_safe.py:167)."""
+    x = np.linspace(-80.0, 80.0, 32001)
+    ours = x / (1.0 + np.exp2(-x * math.log2(math.e)))
+    ref = F.silu(torch.from_numpy(x)).numpy()
+    assert np.max(np.abs(ours - ref) / np.maximum(np.abs(ref), 1e-300)) < 1e-14
+    assert np.max(np.abs(x / (1.0 + np.exp2(x * math.log2(math.e))) - ref)) > 1.0   # sign of the exponent
+
+
+def test_gated_mlp_matches_the_reference_loop():
+    """Plain linears: gate, up = fc1(rows).chunk(2, -1); fc2(F.silu(gate.float()) * up.float())
+    per chunk, in x's dtype (fp16_safe.py:126-172)."""
+    torch.manual_seed(1)
+    fc1, fc2 = nn.Linear(64, 2 * 80), nn.Linear(80, 48)
+    x = torch.randn(3, 41, 64)
+    gate, up = fc1(x.reshape(-1, 64)).chunk(2, -1)
+    ref = fc2(F.silu(gate.float()) * up.float()).reshape(3, 41, 48)
+    for chunk in (None, 1, 7, 123, 1000):
+        assert torch.allclose(mlp.gated_mlp(fc1, fc2, x, chunk_tokens=chunk), ref, rtol=0, atol=1e-6)
+    assert mlp.gated_mlp(fc1, fc2, x[:0]).shape == (0, 41, 48)
+    with pytest.raises(ValueError):
+        mlp.gated_mlp(fc1, fc2, x, chunk_tokens=0)
+
+
+def test_gated_mlp_with_quant_linears_on_cpu():
+    fc1 = _layer(128, 256, "int8", {"convrot": True, "convrot_groupsize": 64}, seed=11)
+    fc2 = _layer(128, 128, "int8", {"convrot": True, "convrot_groupsize": 64}, seed=12)
+    x = torch.randn(37, 128, generator=seeded(13)).to(torch.bfloat16)
+    h = fc1.forward_act(x, "silu_gate")
+    gate, up = fc1(x).chunk(2, -1)
+    assert h.dtype == torch.float32 and torch.equal(h, F.silu(gate.float()) * up.float())
+    ref = fc2(F.silu(gate.float()) * up.float())
+    out = mlp.gated_mlp(fc1, fc2, x, chunk_tokens=16)
+    assert out.dtype == torch.bfloat16 and torch.equal(out, ref)
+    odd = _layer(128, 95, "int8", {"convrot": True, "convrot_groupsize": 64}, seed=14)
+    with pytest.raises(ValueError):
+        odd.forward_act(x, "silu_gate")
