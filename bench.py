@@ -44,10 +44,14 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # ~60 ms of warm-up at the headline shape: the GPU's clock ramps over the first ~30 launches
+    # after an idle spell (2.4 ms -> 1.75 ms per GEMM launch), and a serving loop runs at the
+    # settled clock
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--extras", default="", help="comma-separated subset of the extra workloads to run "
-                    "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, shard_m4095, wan14b_stack); default all")
+                    "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, h3_mlp_silu_gate, shard_m4095, wan14b_stack); "
+                    "default all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample time")
     ap.add_argument("--calibrate-copy", action="store_true",
