@@ -65,3 +65,29 @@ def test_int8linear_unsupported_shape_uses_tiles(gpu):
     tiles = make(336, 48, False, 16, gpu, seed=4)
     tiles._ps_native = False
     torch.testing.assert_close(y, tiles(x))
+
+
+@pytest.mark.parametrize("safe", [False, True])
+def test_prepared_linears_on_the_gpu_tile_path(gpu, safe):
+    """operations.py:158-191 on the GPU: Int8Linear on its tile path (the fp32 island, or the kernels
+    switched off) dequantizes its tiles once per MLP through the dequant kernel; the outputs equal
+    the per-call tiles' bit for bit, and the cache is dropped on exit.  On the kernel path nothing is
+    prepared."""
+    from powershard_amd import mlp
+    from powershard_amd.operations import prepared_linears
+    fc1, fc2 = make(512, 256, True, 256, gpu, seed=71), make(256, 128, True, 256, gpu, seed=72)
+    for m in (fc1, fc2):
+        if safe:
+            m._ps_safe, m._ps_fp32 = True, False
+        else:
+            m._ps_native = False
+    x = (torch.randn(300, 512, generator=seeded(73))).half().to(gpu)
+    ref = mlp.chunked_mlp(fc1, fc2, x, chunk_tokens=64)
+    with prepared_linears((fc1, fc2), budget=1 << 30) as info:
+        assert info["prepared_weight_bytes"] == (512 * 256 + 256 * 128) * (4 if safe else 2)
+        assert fc1._ps_prepared[0].device.type == "cuda"
+    out = mlp.chunked_mlp(fc1, fc2, x, chunk_tokens=64, prepare_budget=1 << 30)
+    assert torch.equal(out, ref) and not hasattr(fc1, "_ps_prepared")
+    native = make(512, 256, True, 256, gpu, seed=74)
+    with prepared_linears((native,), budget=1 << 30) as info:
+        assert info["prepared_weight_bytes"] == 0 and not hasattr(native, "_ps_prepared")
