@@ -485,18 +485,61 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                     // epilogue below: whole-line stores
                     uint8_t *const eb = smem + kEpiOffset + wave * EPI_WAVE_BYTES;
                     const int h = lane >> 5;
+                    // the operand words of column group (jj, pr) (scales and bias words of columns
+                    // nc, nc + 8 of the gate and nc + 64, nc + 72 of the up half), read one group
+                    // ahead so that their LDS latency overlaps the current group's conversion
+                    auto graw = [&](int g, v4i (&w)[8]) {
+                        const int nc = 32 * ((g >> 1) & 1) + 16 * (g & 1);
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int off = nc + 8 * (q & 1) + 64 * (q >> 1);
+                            w[q] = *(const v4i *)(sc + BM + nl0 + off);
+                            w[4 + q] = *(const v4i *)(sc + BM + BN + nl0 + off);
+                        }
+                    };
+                    auto gconv = [&](const v4i (&w)[8], float (&ws)[4][4], float (&bs)[4][4]) {
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+#pragma unroll
+                            for (int c = 0; c < 4; c++) ws[q][c] = __int_as_float(w[q][c]);
+                        if (!ep.bias) {
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+#pragma unroll
+                                for (int c = 0; c < 4; c++) bs[q][c] = 0.0f;
+                        } else if (ep.bias_dtype == PSQ_BF16) {
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+#pragma unroll
+                                for (int c = 0; c < 4; c++) bs[q][c] = __uint_as_float((uint32_t)w[4 + q][c] << 16);
+                        } else if (ep.bias_dtype == PSQ_F16) {
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+#pragma unroll
+                                for (int c = 0; c < 4; c++) bs[q][c] = f16_to_f32((uint32_t)w[4 + q][c]);
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+#pragma unroll
+                                for (int c = 0; c < 4; c++) bs[q][c] = __int_as_float(w[4 + q][c]);
+                        }
+                    };
+                    v4i graw_buf[2][8];
+                    graw(0, graw_buf[0]);
 #pragma unroll
                     for (int i = 0; i < TM; i++) {
 #pragma unroll
                         for (int jj = 0; jj < 2; jj++)
 #pragma unroll
                             for (int pr = 0; pr < 2; pr++) {
-                                const int nc = 32 * jj + 16 * pr;
-                                float wg[2][4], bg[2][4], wu[2][4], bu[2][4];
-                                operands(nc, wg[0], bg[0]);
-                                operands(nc + 8, wg[1], bg[1]);
-                                operands(nc + 64, wu[0], bu[0]);
-                                operands(nc + 72, wu[1], bu[1]);
+                                const int g = 4 * i + 2 * jj + pr;
+                                float ws4[4][4], bs4[4][4];
+                                gconv(graw_buf[g & 1], ws4, bs4);
+                                if (g + 1 < 4 * TM) graw(g + 1, graw_buf[(g + 1) & 1]);
+                                float (&wg)[2][4] = *reinterpret_cast<float (*)[2][4]>(&ws4[0]);
+                                float (&bg)[2][4] = *reinterpret_cast<float (*)[2][4]>(&bs4[0]);
+                                float (&wu)[2][4] = *reinterpret_cast<float (*)[2][4]>(&ws4[2]);
+                                float (&bu)[2][4] = *reinterpret_cast<float (*)[2][4]>(&bs4[2]);
                                 uint32_t x[2], y[2];
 #pragma unroll
                                 for (int hh = 0; hh < 2; hh++) {
