@@ -1018,7 +1018,8 @@ int check_shapes(const char *name, const void *a, int64_t lda, const void *w, in
                  int64_t K)
 {
     if (M < 0 || N < 0 || K < 0) return set_error(PSQ_E_ARG, "%s: negative size", name);
-    if (!a || !w) return set_error(PSQ_E_ARG, "%s: null operand", name);
+    // an empty problem reads nothing: empty tensors may come with null data pointers
+    if (M > 0 && N > 0 && (!a || !w)) return set_error(PSQ_E_ARG, "%s: null operand", name);
     if (K == 0 || K % 128)
         return set_error(PSQ_E_SHAPE, "%s: K=%lld must be a positive multiple of 128", name, (long long)K);
     if (lda < K || ldw < K || lda % 16 || ldw % 16)

@@ -823,7 +823,8 @@ int check_common(const char *name, const void *x, int x_dtype, int64_t ldx, cons
                  int64_t ldy, const void *bias, int bias_dtype, int64_t M, int64_t N, int64_t K)
 {
     if (M < 0 || N < 0 || K < 0) return set_error(PSQ_E_ARG, "%s: negative size", name);
-    if (!x || !wq || !y) return set_error(PSQ_E_ARG, "%s: null pointer", name);
+    // an empty problem touches nothing: empty tensors may come with null data pointers
+    if (M > 0 && N > 0 && (!x || !wq || !y)) return set_error(PSQ_E_ARG, "%s: null pointer", name);
     if (x_dtype != PSQ_BF16 && x_dtype != PSQ_F16) return set_error(PSQ_E_ARG, "%s: activations must be bf16/f16", name);
     if (!valid_dtype(y_dtype) || (bias && !valid_dtype(bias_dtype))) return set_error(PSQ_E_ARG, "%s: bad dtype", name);
     if (K == 0 || K % KSTAGE) return set_error(PSQ_E_SHAPE, "%s: K=%lld must be a positive multiple of %d", name, (long long)K, KSTAGE);

@@ -69,6 +69,16 @@ def test_empty_problems_are_no_ops():
     lib = _native.lib()
     assert lib.psq_gemm_i8(_fake(), 128, _fake(), _fake(), 128, _fake(), None, 0, _fake(), 0, 16, 0, 16, 128, None) == 0
     assert lib.psq_quantize_rows_i8(_fake(), 0, 0, 512, 512, 256, None, _fake(), 512, _fake(), None) == 0
+    # empty tensors come with null data pointers (torch.empty((0, K)).data_ptr() == 0)
+    assert lib.psq_gemm_i8(None, 128, None, _fake(), 128, _fake(), None, 0, None, 0, 16, 0, 16, 128, None) == 0
+    assert lib.psq_gemm_i8_act(None, 128, None, _fake(), 128, _fake(), None, 0, 2, None, 0, 64, 0, 128, 128, None) == 0
+    assert lib.psq_gemm_fp8(None, 128, None, _fake(), 128, _fake(), 0, None, 0, None, 0, 16, 0, 16, 128, None) == 0
+    assert lib.psq_gemm_w4a16(None, 0, 128, _fake(), _fake(), _fake(), 128, None, 0, None, 0, 16, 0, 16, 128, None) == 0
+    assert lib.psq_gemm_w8a16(None, 0, 128, _fake(), _fake(), None, 0, None, 0, 16, 0, 16, 128, None) == 0
+    assert lib.psq_quantize_rows_i8(None, 0, 0, 512, 512, 256, None, None, 512, None, None) == 0
+    assert lib.psq_rotate_rows(None, 0, 0, 512, 512, 256, None, 0, 512, None) == 0
+    # a non-empty problem with a null operand is still an error
+    assert lib.psq_gemm_i8(None, 128, _fake(), _fake(), 128, _fake(), None, 0, _fake(), 0, 16, 4, 16, 128, None) == -1
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

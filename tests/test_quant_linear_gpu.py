@@ -177,3 +177,34 @@ def test_reuse_quantized_inputs(gpu, weight_format, opts):
     with torch.no_grad():
         assert torch.equal(got3.view(torch.int16), layers[0](x).view(torch.int16))
         assert torch.equal(got4.view(torch.int16), layers[1](x).view(torch.int16))
+
+
+@pytest.mark.parametrize("weight_format,opts", [("int8", {"convrot": True, "convrot_groupsize": 256}),
+                                                ("fp8", {}), ("int4", {"group_size": 128})])
+def test_empty_batch_stays_native(gpu, weight_format, opts):
+    """An empty token batch (empty tensors have null data pointers) is a no-op for every kernel:
+    the module returns [0, N] (and [0, N / 2] for the gate) and keeps its native path."""
+    layer, _, _ = make_layer(256, 256, weight_format, opts, torch.bfloat16, True, gpu, seed=81)
+    x = torch.empty(0, 256, dtype=torch.bfloat16, device=gpu)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        y = layer(x)
+        assert y.shape == (0, 256) and layer._ps_native
+        if weight_format != "int4":
+            assert layer.forward_act(x, "gelu_tanh").shape == (0, 256)
+            assert layer.forward_act(x, "silu_gate").shape == (0, 128)
+        y3 = layer(torch.empty(2, 0, 256, dtype=torch.bfloat16, device=gpu))
+        assert y3.shape == (2, 0, 256) and layer._ps_native
+    torch.cuda.synchronize()
+
+
+def test_empty_batch_int8linear_stays_on_the_kernels(gpu):
+    from powershard_amd.operations import Int8Linear
+    src = torch.nn.Linear(512, 256)
+    layer = Int8Linear(src, dict(convrot=True, group_size=256), rows=64).to_empty(device=gpu)
+    layer.weight.data.copy_(torch.randint(-127, 128, (256, 512), generator=seeded(82), dtype=torch.int8))
+    layer.weight_scale.data.copy_(torch.rand(256, 1, generator=seeded(83)) * 1e-3 + 1e-4)
+    layer.bias = torch.nn.Parameter(torch.zeros(256, dtype=torch.float16, device=gpu), requires_grad=False)
+    y = layer(torch.empty(0, 512, dtype=torch.float16, device=gpu))
+    torch.cuda.synchronize()
+    assert y.shape == (0, 256) and getattr(layer, "_ps_native", True)
