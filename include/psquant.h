@@ -6,7 +6,8 @@
  * caller's stream (`stream` is a hipStream_t passed as void*; NULL = the null stream).
  * Every function returns 0 on success and a negative PSQ_E* code on failure, after which
  * psq_last_error() returns a message for the calling thread.  Entry points are re-entrant
- * and hold no per-call state.
+ * and hold no per-call state.  A problem with no rows or no columns (M or N zero) is a no-op
+ * that succeeds whatever its data pointers (empty tensors may have null ones).
  *
  * Reference interfaces replaced (ComfyUI-PowerShard 0.6.0):
  *   - powershard/quant_linear.py:230-242 native_linear() -> comfy-kitchen ops
