@@ -68,11 +68,17 @@ def _dt(t, what):
 
 
 def _rows2d(x):
-    """[M, K] view with unit column stride and 16-byte aligned rows (copies if needed)."""
+    """[M, K] with unit column stride, rows at least K apart and 16-byte aligned rows: x itself
+    when it is so laid out, else a packed copy (torch's contiguous() keeps the strides of size-1
+    dimensions and the offset of an aligned-looking view, so the copy is explicit)."""
     if x.dim() != 2:
         raise ValueError("expected a 2-D tensor")
-    if x.stride(1) != 1 or (x.stride(0) * x.element_size()) % 16 or x.data_ptr() % 16:
-        x = x.contiguous()
+    M, K = x.shape
+    if M == 0 or K == 0:
+        return x
+    if (x.stride(1) != 1 or x.stride(0) < K or (x.stride(0) * x.element_size()) % 16
+            or x.data_ptr() % 16):
+        x = torch.empty((M, K), dtype=x.dtype, device=x.device).copy_(x)
     return x
 
 

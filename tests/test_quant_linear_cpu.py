@@ -456,3 +456,26 @@ def test_chunked_mlp_prepares_tiles_once_per_mlp(monkeypatch):
     count = 0
     mlp.chunked_mlp(fc1, fc2, x, prepare_budget=1 << 30)         # one chunk: nothing prepared
     assert count == 64 // 8 + 16 // 8
+
+
+def test_rows2d_packs_what_the_kernels_cannot_address():
+    """The kernels address rows as base + m * ld with ld >= K, a multiple of 16 bytes, and a
+    16-byte aligned base; every other layout is copied, the values unchanged."""
+    from powershard_amd.ops import _rows2d
+    base = torch.randn(8, 300)
+    cases = {
+        "packed": base[:, :256].contiguous(),
+        "row slice": base[:, :256],                                   # ld 300: 1200 B, not 16-aligned
+        "offset view": base.reshape(-1)[1:1 + 4 * 256].view(4, 256),  # base 4 B past an aligned one
+        "broadcast rows": base[0, :256].expand(5, 256),               # ld 0
+        "one column-major row": torch.randn(256, 1).t(),              # [1, 256] with ld 1
+        "transposed": base[:, :8].t(),
+    }
+    for name, x in cases.items():
+        y = _rows2d(x)
+        assert torch.equal(y, x), name
+        assert y.stride(1) == 1 and y.stride(0) >= y.shape[1], name
+        assert (y.stride(0) * y.element_size()) % 16 == 0 and y.data_ptr() % 16 == 0, name
+    packed = cases["packed"]
+    assert _rows2d(packed).data_ptr() == packed.data_ptr()          # no copy when not needed
+    assert _rows2d(torch.empty(0, 256)).shape == (0, 256)

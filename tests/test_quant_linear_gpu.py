@@ -208,3 +208,21 @@ def test_empty_batch_int8linear_stays_on_the_kernels(gpu):
     y = layer(torch.empty(0, 512, dtype=torch.float16, device=gpu))
     torch.cuda.synchronize()
     assert y.shape == (0, 256) and getattr(layer, "_ps_native", True)
+
+
+@pytest.mark.parametrize("weight_format,opts", [("int8", {"convrot": True, "convrot_groupsize": 256}),
+                                                ("fp8", {}), ("int4", {"group_size": 128})])
+def test_strided_inputs_stay_native(gpu, weight_format, opts):
+    """Row slices, offset views and broadcast rows reach the kernels as packed copies: the same
+    output as the contiguous input, bit for bit, and the module keeps its native path."""
+    layer, _, _ = make_layer(256, 384, weight_format, opts, torch.bfloat16, True, gpu, seed=91)
+    wide = heavy_rows(64, 300, seed=92).to(gpu)
+    flat = wide.reshape(-1)
+    inputs = [wide[:, :256], flat[1:1 + 48 * 256].view(48, 256), wide[0, :256].expand(7, 256)]
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        for x in inputs:
+            y = layer(x)
+            ref = layer(x.contiguous().clone())
+            assert layer._ps_native
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
