@@ -470,8 +470,8 @@ def extra_w8a16(args):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build measures one GPU: the quantized linear path has no multi-GPU "
-                                   "code (see DESIGN.md for how it would shard); run with --gpus 1"}))
+        print(json.dumps({"error": "one GPU only: the quantized linear path here has no multi-GPU code "
+                                   "(its sharding is a design, not an implementation); run with --gpus 1"}))
         sys.exit(2)
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False

@@ -1,8 +1,8 @@
 """CPU oracle for the quantized linear path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
-this package, and only as the checker.  The product (``comfyui-powershard_amd/powershard_amd``)
-never imports it and has no CPU fallback through it.
+this package, and only to check or time results, never to produce them.  The product
+(``comfyui-powershard_amd/powershard_amd``) never imports it and has no CPU fallback through it.
 
 Two layers:
 

@@ -1,7 +1,7 @@
 /*
  * psq_oracle.c -- CPU oracle for the quantized linear path (TEST INFRASTRUCTURE ONLY).
  *
- * This file is the checker, never the product: only tests/, __graft_entry__.smoke() and
+ * It checks the product and is never part of it: only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg may load it.  The HIP library must never call into it.
  *
  * It restates, in plain C with OpenMP, the arithmetic of PowerShard's quantized linear
