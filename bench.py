@@ -66,32 +66,33 @@ def gen(seed):
     return torch.Generator(device="cuda").manual_seed(seed)
 
 
-def activations(M, K, cfg, outlier_scale=20.0, student_t=False, dev="cuda"):
-    """bf16 [M, K]: N(0,1) (or Student-t, df=3) with 1% of channels (seeded pick) scaled."""
+def activations(M, K, sid, outlier_scale=20.0, student_t=False, dev="cuda"):
+    """bf16 [M, K]: N(0,1) (or Student-t, df=3) with 1% of channels (seeded pick) scaled; `sid`
+    offsets the seeds so that each workload draws its own synthetic inputs."""
     import torch
-    g = gen(2000 + cfg)
+    g = gen(2000 + sid)
     x = torch.randn(M, K, generator=g, device=dev)
     if student_t:
         chi = torch.zeros_like(x)
         for _ in range(3):
             chi += torch.randn(M, K, generator=g, device=dev) ** 2
         x /= (chi / 3).sqrt()
-    gp = torch.Generator().manual_seed(4000 + cfg)
+    gp = torch.Generator().manual_seed(4000 + sid)
     idx = torch.randperm(K, generator=gp)[: int(0.01 * K)].to(dev)
     x[:, idx] *= outlier_scale
     return x.to(torch.bfloat16)
 
 
-def quant_layer(K, N, weight_format, cfg, seed=None, opts=None, dev="cuda", dtype=None):
+def quant_layer(K, N, weight_format, sid, seed=None, opts=None, dev="cuda", dtype=None):
     """A QuantLinear installed and filled through the package's own install/pack path (compute
     dtype bf16 unless given)."""
     import torch
     from torch import nn
     from powershard_amd.quant_linear import install_quant_linears, quantized_from_float, pack
-    g = gen(1000 + cfg if seed is None else seed)
+    g = gen(1000 + sid if seed is None else seed)
     w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     dtype = dtype or torch.bfloat16
-    b = (torch.randn(N, generator=gen(3000 + cfg), device=dev) * 0.01).to(dtype)
+    b = (torch.randn(N, generator=gen(3000 + sid), device=dev) * 0.01).to(dtype)
     with torch.device("meta"):
         net = nn.Sequential(nn.Linear(K, N, dtype=dtype))
     tensors = {"0.weight": {"key": "0.weight", "dtype": "BF16", "shape": [N, K]}}
@@ -144,10 +145,10 @@ def untimed_kernel_ms(step, steps, warmup):
 def headline(args):
     import torch
     M, K, N = 32760, 5120, 13824
-    cfg = 1
+    sid = 1
     log(f"[bench] headline W8A8+ConvRot M={M} K={K} N={N}: building inputs")
-    x = activations(M, K, cfg)
-    layer, qt, b = quant_layer(K, N, "int8", cfg, opts={"convrot": True, "convrot_groupsize": 256})
+    x = activations(M, K, sid)
+    layer, qt, b = quant_layer(K, N, "int8", sid, opts={"convrot": True, "convrot_groupsize": 256})
     with torch.no_grad():
         y = layer(x)
     if not layer._ps_native:
@@ -172,7 +173,7 @@ def headline(args):
         f"({100 * gemm_tops / PEAK_INT8_TOPS:.1f}% of int8 peak); quant {quant_ms * 1e3:.1f} us = "
         f"{res['quant_gbs']:.0f} GB/s")
     # parity rows: the first 64, 128 spread over the middle, and the last 64 (the partial last tile)
-    g = torch.Generator().manual_seed(5000 + cfg)
+    g = torch.Generator().manual_seed(5000 + sid)
     mid = torch.randperm(M - 128, generator=g)[:128] + 64
     idx = torch.cat([torch.arange(64), mid.sort().values, torch.arange(M - 64, M)])
     sample = dict(x=x[:8192].cpu(), qdata=qt._qdata.cpu(), scale=qt._params.scale.cpu(), bias=b.cpu(),
@@ -241,11 +242,11 @@ def extra_int4(args):
     """W4A16 uint4 g128 Qwen3-VL-32B text-encoder MLP, K=5120 -> N=25600; M sweep; MALL-defeating
     rotation over 4 distinct weight copies (4 x 69.6 MB > 256 MB Infinity Cache)."""
     import torch
-    K, N, cfg = 5120, 25600, 2
-    layers = [quant_layer(K, N, "int4", cfg, seed=1000 + cfg + 17 * i, opts={"group_size": 128})[0] for i in range(4)]
+    K, N, sid = 5120, 25600, 2
+    layers = [quant_layer(K, N, "int4", sid, seed=1000 + sid + 17 * i, opts={"group_size": 128})[0] for i in range(4)]
     out = {}
     for M in (1, 16, 64, 128, 256, 512):
-        x = activations(M, K, cfg, outlier_scale=1.0)
+        x = activations(M, K, sid, outlier_scale=1.0)
         it = [0]
 
         def step():
@@ -268,9 +269,9 @@ def extra_int4(args):
 
 def extra_fp8(args):
     import torch
-    M, K, N, cfg = 32760, 5120, 15360, 3
-    x = activations(M, K, cfg, outlier_scale=1.0)
-    layer = quant_layer(K, N, "fp8", cfg)[0]
+    M, K, N, sid = 32760, 5120, 15360, 3
+    x = activations(M, K, sid, outlier_scale=1.0)
+    layer = quant_layer(K, N, "fp8", sid)[0]
 
     def step():
         with torch.no_grad():
@@ -293,20 +294,20 @@ def extra_wan_stack(args):
     heavy-tailed inputs (Student-t df=3, 1% channels x50); random-init int8 weights per block.
     Four activation quantizations per block: q, k and v share theirs (reuse_quantized_inputs)."""
     import torch
-    M, D, F, cfg = 32760, 5120, 13824, 4
+    M, D, F, sid = 32760, 5120, 13824, 4
     opts = {"convrot": True, "convrot_groupsize": 256}
     blocks = []
     for blk in range(40):
-        seed = 1000 + cfg + 1000 * blk
-        q = quant_layer(D, D, "int8", cfg, seed=seed + 1, opts=opts)[0]
-        k = quant_layer(D, D, "int8", cfg, seed=seed + 2, opts=opts)[0]
-        v = quant_layer(D, D, "int8", cfg, seed=seed + 3, opts=opts)[0]
-        o = quant_layer(D, D, "int8", cfg, seed=seed + 4, opts=opts)[0]
-        up = quant_layer(D, F, "int8", cfg, seed=seed + 5, opts=opts)[0]
-        down = quant_layer(F, D, "int8", cfg, seed=seed + 6, opts=opts)[0]
+        seed = 1000 + sid + 1000 * blk
+        q = quant_layer(D, D, "int8", sid, seed=seed + 1, opts=opts)[0]
+        k = quant_layer(D, D, "int8", sid, seed=seed + 2, opts=opts)[0]
+        v = quant_layer(D, D, "int8", sid, seed=seed + 3, opts=opts)[0]
+        o = quant_layer(D, D, "int8", sid, seed=seed + 4, opts=opts)[0]
+        up = quant_layer(D, F, "int8", sid, seed=seed + 5, opts=opts)[0]
+        down = quant_layer(F, D, "int8", sid, seed=seed + 6, opts=opts)[0]
         blocks.append((q, k, v, o, up, down))
-    x = activations(M, D, cfg, outlier_scale=50.0, student_t=True)
-    h = activations(M, F, cfg + 100, outlier_scale=50.0, student_t=True)
+    x = activations(M, D, sid, outlier_scale=50.0, student_t=True)
+    h = activations(M, F, sid + 100, outlier_scale=50.0, student_t=True)
 
     from powershard_amd.quant_linear import reuse_quantized_inputs
 
@@ -335,11 +336,11 @@ def extra_ffn(args):
     cast to bf16 by down) against the GELU in the up-projection's epilogue (up.forward_act)."""
     import torch
     import torch.nn.functional as Fn
-    M, D, F, cfg = 32760, 5120, 13824, 4
+    M, D, F, sid = 32760, 5120, 13824, 4
     opts = {"convrot": True, "convrot_groupsize": 256}
-    up = quant_layer(D, F, "int8", cfg, seed=1000 + cfg + 5, opts=opts)[0]
-    down = quant_layer(F, D, "int8", cfg, seed=1000 + cfg + 6, opts=opts)[0]
-    x = activations(M, D, cfg, outlier_scale=50.0, student_t=True)
+    up = quant_layer(D, F, "int8", sid, seed=1000 + sid + 5, opts=opts)[0]
+    down = quant_layer(F, D, "int8", sid, seed=1000 + sid + 6, opts=opts)[0]
+    x = activations(M, D, sid, outlier_scale=50.0, student_t=True)
     steps = max(3, min(args.steps, 10))
     res = {"workload": "Wan-14B FFN up 5120->13824, GELU(tanh), down 13824->5120, W8A8+ConvRot, M=32760"}
     with torch.no_grad():
@@ -365,13 +366,13 @@ def extra_h3_mlp(args):
     fc2(F.silu(gate.float()) * up.float()) against the gate in fc1's epilogue."""
     import torch
     import torch.nn.functional as Fn
-    M, D, F, cfg = 8192, 5376, 14336, 5
+    M, D, F, sid = 8192, 5376, 14336, 5
     opts = {"convrot": True, "convrot_groupsize": 256}
-    fc1 = quant_layer(D, 2 * F, "int8", cfg, seed=5000, opts=opts, dtype=torch.float16)[0]
-    fc2 = quant_layer(F, D, "int8", cfg, seed=5001, opts=opts, dtype=torch.float16)[0]
+    fc1 = quant_layer(D, 2 * F, "int8", sid, seed=5000, opts=opts, dtype=torch.float16)[0]
+    fc2 = quant_layer(F, D, "int8", sid, seed=5001, opts=opts, dtype=torch.float16)[0]
     # N(0,1) with 1% of channels x20: fc1's outputs stay well inside fp16 (heavier tails overflow
     # the fp16 hidden of the reference sequence itself)
-    x = activations(M, D, cfg).to(torch.float16)
+    x = activations(M, D, sid).to(torch.float16)
     steps = max(3, min(args.steps, 10))
 
     def unfused():
@@ -400,7 +401,7 @@ def extra_shard(args):
     the headline QuantLinear forward and one Wan block of W8A8+ConvRot linears at that M, to set
     against the single-GPU figures when planning the sharded path (one GPU runs it here)."""
     import torch
-    M, D, F, cfg = 4095, 5120, 13824, 4
+    M, D, F, sid = 4095, 5120, 13824, 4
     opts = {"convrot": True, "convrot_groupsize": 256}
     from powershard_amd.quant_linear import reuse_quantized_inputs
     up = quant_layer(D, F, "int8", 1, opts=opts)[0]
@@ -408,10 +409,10 @@ def extra_shard(args):
     steps = max(10, args.steps)
     with torch.no_grad():
         fwd_ms = untimed_kernel_ms(lambda: up(x), steps, 3)
-    layers = [quant_layer(D, D, "int8", cfg, seed=2000 + i, opts=opts)[0] for i in range(4)]
-    down = quant_layer(F, D, "int8", cfg, seed=2010, opts=opts)[0]
-    xs = activations(M, D, cfg, outlier_scale=50.0, student_t=True)
-    h = activations(M, F, cfg + 100, outlier_scale=50.0, student_t=True)
+    layers = [quant_layer(D, D, "int8", sid, seed=2000 + i, opts=opts)[0] for i in range(4)]
+    down = quant_layer(F, D, "int8", sid, seed=2010, opts=opts)[0]
+    xs = activations(M, D, sid, outlier_scale=50.0, student_t=True)
+    h = activations(M, F, sid + 100, outlier_scale=50.0, student_t=True)
     q, k, v, o = layers
 
     def block():
@@ -433,10 +434,10 @@ def extra_shard(args):
 
 def extra_w8a16(args):
     import torch
-    M, K, N, cfg = 1024, 5120, 5120, 0
+    M, K, N, sid = 1024, 5120, 5120, 0
     from powershard_amd import ops
-    x = activations(M, K, cfg, outlier_scale=1.0)
-    layer, qt, b = quant_layer(K, N, "int8", cfg)
+    x = activations(M, K, sid, outlier_scale=1.0)
+    layer, qt, b = quant_layer(K, N, "int8", sid)
     q, s = qt._qdata, qt._params.scale
 
     def step():
