@@ -106,6 +106,22 @@ def quant_layer(K, N, weight_format, sid, seed=None, opts=None, dev="cuda", dtyp
     return layer, qt, b
 
 
+def fused_vs_reference(got, ref):
+    """Errors of a fused MLP against the reference sequence on the same modules: max and RMS of the
+    difference over the output RMS, and whether every element is within max(1e-2 RMS, one bf16 ulp
+    of the reference value).  A hidden element one ulp away can move its row's per-token scale in
+    the down projection, which shifts that row by up to a quantization step: on heavy-tailed rows
+    that exceeds 1e-2 RMS only where one ulp of the output itself does."""
+    import torch
+    got, ref = got.float(), ref.float()
+    rms = ref.pow(2).mean().sqrt()
+    err = (got - ref).abs()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(ref.abs().clamp(min=1e-30))) - 7)
+    bound = torch.maximum(1e-2 * rms, ulp)
+    return dict(max_err_over_rms=(err.max() / rms).item(), rms_err_over_rms=(err.pow(2).mean().sqrt() / rms).item(),
+                within_bar=bool((err <= bound).all().item()), frac_over_1e2_rms=(err > 1e-2 * rms).double().mean().item())
+
+
 # ---------------------------------------------------------------------- timing
 def timed_steps(step, steps, warmup):
     """(ms per step from events around the whole loop, {kernel: mean ms per launch})."""
@@ -351,9 +367,10 @@ def extra_ffn(args):
         res["up_gelu_ms"] = untimed_kernel_ms(lambda: up.forward_act(x), steps, 1)
         ref = down(Fn.gelu(up(x).float(), approximate="tanh")).float()
         got = down(up.forward_act(x)).float()
-        res["max_err_over_rms"] = ((got - ref).abs().max() / ref.pow(2).mean().sqrt()).item()
+        res.update(fused_vs_reference(got, ref))
     log(f"[bench] wan ffn: unfused {res['unfused_ms']:.3f} ms, fused {res['fused_ms']:.3f} ms; up GEMM "
-        f"{res['up_ms']:.3f} ms, with GELU {res['up_gelu_ms']:.3f} ms; max err/rms {res['max_err_over_rms']:.2e}")
+        f"{res['up_ms']:.3f} ms, with GELU {res['up_gelu_ms']:.3f} ms; max err/rms {res['max_err_over_rms']:.2e}, "
+        f"rms err/rms {res['rms_err_over_rms']:.2e}, within max(1e-2 rms, 1 ulp): {res['within_bar']}")
     del up, down, x
     torch.cuda.empty_cache()
     return res
@@ -388,9 +405,10 @@ def extra_h3_mlp(args):
         got = fc2(fc1.forward_act(x, "silu_gate")).float()
         if not (torch.isfinite(ref).all() and torch.isfinite(got).all()):
             raise RuntimeError("h3 mlp: non-finite outputs")
-        res["max_err_over_rms"] = ((got - ref).abs().max() / ref.pow(2).mean().sqrt()).item()
+        res.update(fused_vs_reference(got, ref))
     log(f"[bench] h3 mlp: unfused {res['unfused_ms']:.3f} ms, fused {res['fused_ms']:.3f} ms; fc1 GEMM "
-        f"{res['fc1_ms']:.3f} ms, with the gate {res['fc1_gate_ms']:.3f} ms; max err/rms {res['max_err_over_rms']:.2e}")
+        f"{res['fc1_ms']:.3f} ms, with the gate {res['fc1_gate_ms']:.3f} ms; max err/rms {res['max_err_over_rms']:.2e}, "
+        f"rms err/rms {res['rms_err_over_rms']:.2e}, within max(1e-2 rms, 1 ulp): {res['within_bar']}")
     del fc1, fc2, x
     torch.cuda.empty_cache()
     return res
