@@ -70,47 +70,54 @@ dequant_fp8_kernel(const uint8_t *__restrict__ q, const float *__restrict__ sc, 
     store16<ODT>(out, n * K + k0, v);
 }
 
-// int8 rows: one workgroup per row, 16 values per thread, ConvRot inverse as in quantize_rows
-// (H is symmetric, so v @ H^T = 2^-k T(v)).
-template <int ODT, int ROTK>
+// int8 rows: one workgroup per row; thread t owns P chunks of 16 consecutive values, chunk c at
+// elements [(c T + t) 16, +16) (T = blockDim.x, a multiple of 64), so each wave covers 1024
+// consecutive values per chunk and ConvRot groups (at most 1024, dividing K) never straddle waves.
+// The ConvRot inverse is the quantizer's transform (H is symmetric, so v @ H^T = 2^-k T(v)).
+// Lanes past K carry zeros through the cross-lane stages: their groups lie wholly past K.
+template <int ODT, int ROTK, int P>
 __global__ void __launch_bounds__(1024)
 dequant_i8_rows_kernel(const int8_t *__restrict__ q, const float *__restrict__ sc, int64_t K, void *__restrict__ out)
 {
     const int64_t n = blockIdx.x;
-    const int t = threadIdx.x;
-    const bool active = (int64_t)t * 16 < K;
-    float v[16];
-    v4i p = {0, 0, 0, 0};
-    if (active) p = *(const v4i *)(q + n * K + (int64_t)t * 16);
+    const int t = threadIdx.x, T = blockDim.x;
     const float s = sc[n];
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = (float)(int8_t)(((uint32_t)p[i >> 2] >> (8 * (i & 3))) & 0xffu) * s;
-    if constexpr (ROTK >= 1) {
+    for (int c = 0; c < P; c++) {
+        const int64_t e0 = (int64_t)(c * T + t) * 16;
+        const bool active = e0 < K;
+        float v[16];
+        v4i p = {0, 0, 0, 0};
+        if (active) p = *(const v4i *)(q + n * K + e0);
 #pragma unroll
-        for (int b = 0; b < 16; b += 4) radix4(v[b], v[b + 1], v[b + 2], v[b + 3]);
-    }
-    if constexpr (ROTK >= 2) {
+        for (int i = 0; i < 16; i++) v[i] = (float)(int8_t)(((uint32_t)p[i >> 2] >> (8 * (i & 3))) & 0xffu) * s;
+        if constexpr (ROTK >= 1) {
 #pragma unroll
-        for (int a = 0; a < 4; a++) radix4(v[a], v[a + 4], v[a + 8], v[a + 12]);
-    }
-    if constexpr (ROTK >= 3) {
+            for (int b = 0; b < 16; b += 4) radix4(v[b], v[b + 1], v[b + 2], v[b + 3]);
+        }
+        if constexpr (ROTK >= 2) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<1>(v[j]);
-    }
-    if constexpr (ROTK >= 4) {
+            for (int a = 0; a < 4; a++) radix4(v[a], v[a + 4], v[a + 8], v[a + 12]);
+        }
+        if constexpr (ROTK >= 3) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<4>(v[j]);
-    }
-    if constexpr (ROTK >= 5) {
+            for (int j = 0; j < 16; j++) v[j] = radix4_lanes<1>(v[j]);
+        }
+        if constexpr (ROTK >= 4) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = radix4_lanes<16>(v[j]);
-    }
-    if constexpr (ROTK > 0) {
-        const float post = __builtin_ldexpf(1.0f, -ROTK);
+            for (int j = 0; j < 16; j++) v[j] = radix4_lanes<4>(v[j]);
+        }
+        if constexpr (ROTK >= 5) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = v[j] * post;
+            for (int j = 0; j < 16; j++) v[j] = radix4_lanes<16>(v[j]);
+        }
+        if constexpr (ROTK > 0) {
+            const float post = __builtin_ldexpf(1.0f, -ROTK);
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = v[j] * post;
+        }
+        if (active) store16<ODT>(out, n * K + e0, v);
     }
-    if (active) store16<ODT>(out, n * K + (int64_t)t * 16, v);
 }
 
 int check_out(const char *name, int64_t N, int64_t K, const void *out, int out_dtype)
@@ -175,7 +182,7 @@ int psq_dequant_i8_rows(const int8_t *q, const float *w_scale, int64_t N, int64_
     if (int e = check_out("dequant_i8_rows", N, K, out, out_dtype)) return e;
     if (N == 0 || K == 0) return PSQ_OK;
     if (!q || !w_scale) return set_error(PSQ_E_ARG, "dequant_i8_rows: null pointer");
-    if (K > 16 * 1024) return set_error(PSQ_E_SHAPE, "dequant_i8_rows: K=%lld > 16384", (long long)K);
+    if (K > 32 * 1024) return set_error(PSQ_E_SHAPE, "dequant_i8_rows: K=%lld > 32768", (long long)K);
     if ((uintptr_t)q & 15) return set_error(PSQ_E_SHAPE, "dequant_i8_rows: weights must be 16-byte aligned");
     if (N > 0x7fffffffLL) return set_error(PSQ_E_SHAPE, "dequant_i8_rows: N too large");
     int rotk = 0;
@@ -187,9 +194,14 @@ int psq_dequant_i8_rows(const int8_t *q, const float *w_scale, int64_t N, int64_
                              rot_group);
     }
     if (int e = require_device()) return e;
-    const int threads = (int)((K / 16 + 63) / 64 * 64);
+    // one 16-value chunk per thread up to K = 16384, two up to 32768
+    const int64_t chunks16 = K / 16;
+    const int P = chunks16 <= 1024 ? 1 : 2;
+    const int threads = (int)(((chunks16 + P - 1) / P + 63) / 64 * 64);
     hipStream_t st = (hipStream_t)stream;
-#define PSQ_DQ(ODT, RK) dequant_i8_rows_kernel<ODT, RK><<<dim3((unsigned)N), dim3(threads), 0, st>>>(q, w_scale, K, out)
+#define PSQ_DQ(ODT, RK)                                                                                     \
+    (P == 1 ? dequant_i8_rows_kernel<ODT, RK, 1><<<dim3((unsigned)N), dim3(threads), 0, st>>>(q, w_scale, K, out) \
+            : dequant_i8_rows_kernel<ODT, RK, 2><<<dim3((unsigned)N), dim3(threads), 0, st>>>(q, w_scale, K, out))
 #define PSQ_DQ_ALL(ODT)                                                                                     \
     switch (rotk) {                                                                                         \
     case 0: PSQ_DQ(ODT, 0); break;                                                                          \

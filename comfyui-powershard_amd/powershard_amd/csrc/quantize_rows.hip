@@ -44,33 +44,37 @@ __device__ __forceinline__ void to_f32(const v4i (&raw)[2], float (&v)[16])
     }
 }
 
-// Largest |v| over the 16 values, NaNs ignored (fmax returns the other operand), as a tree.
+// Largest |v| over the 16 values, NaN if any is NaN (IEEE maximum: gfx950's v_maximum3_f32 with
+// |.| source modifiers, two values per instruction).  A row holding a NaN thereby gets a NaN scale,
+// as torch's amax gives, and its dequantized output is NaN.
 __device__ __forceinline__ float absmax16(const float (&v)[16])
 {
-    float m[8];
+    float m = __builtin_elementwise_maximum(__builtin_fabsf(v[0]), __builtin_fabsf(v[1]));
 #pragma unroll
-    for (int j = 0; j < 8; j++) m[j] = __builtin_fmaxf(__builtin_fabsf(v[2 * j]), __builtin_fabsf(v[2 * j + 1]));
-#pragma unroll
-    for (int w = 4; w >= 1; w >>= 1)
-#pragma unroll
-        for (int j = 0; j < w; j++) m[j] = __builtin_fmaxf(m[j], m[j + w]);
-    return m[0];
+    for (int j = 2; j < 16; j += 2)
+        m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(__builtin_fabsf(v[j]), __builtin_fabsf(v[j + 1])));
+    return m;
 }
 
-// Wave-wide max of non-negative, non-NaN values: DPP within rows of 16 lanes, then the
-// gfx950 row swaps across rows (no LDS, no index arithmetic).
-__device__ __forceinline__ float wave_max_dpp(float v)
+// Wave-wide max of non-negative values (a NaN wins): the bit patterns of non-negative floats order
+// as unsigned integers like their values, and a positive NaN's pattern lies above +inf's.  DPP within
+// rows of 16 lanes, then the gfx950 row swaps across rows (no LDS, no index arithmetic).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
 {
-    v = __builtin_fmaxf(v, dpp<DPP_QUAD_XOR1>(v));
-    v = __builtin_fmaxf(v, dpp<DPP_QUAD_XOR2>(v));
-    v = __builtin_fmaxf(v, dpp<DPP_ROW_HALF_MIRROR>(v));   // lane ^ 7: the other quad of the 8
-    v = __builtin_fmaxf(v, dpp<DPP_ROW_MIRROR>(v));        // lane ^ 15: the other 8 of the row
-    const uint32_t u = __float_as_uint(v);
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+
+__device__ __forceinline__ uint32_t wave_max_bits(uint32_t u)
+{
+    u = max(u, dpp_u32<DPP_QUAD_XOR1>(u));
+    u = max(u, dpp_u32<DPP_QUAD_XOR2>(u));
+    u = max(u, dpp_u32<DPP_ROW_HALF_MIRROR>(u));   // lane ^ 7: the other quad of the 8
+    u = max(u, dpp_u32<DPP_ROW_MIRROR>(u));        // lane ^ 15: the other 8 of the row
     const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);   // rows 0 <-> 1, 2 <-> 3
-    v = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const uint32_t w = __float_as_uint(v);
-    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);   // halves
-    return __builtin_fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    u = max((uint32_t)a[0], (uint32_t)a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);   // halves
+    return max((uint32_t)b[0], (uint32_t)b[1]);
 }
 
 // int8 code of u r: clamp to [-127, 127] (equal to clamping after rounding, the bounds being
@@ -134,7 +138,7 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
                      const float *__restrict__ static_scale, uint8_t *__restrict__ q, int64_t ldq,
                      float *__restrict__ scale)
 {
-    __shared__ float wave_amax[R][kMaxThreads / 64];
+    __shared__ uint32_t wave_amax[R][kMaxThreads / 64];
     const int t = threadIdx.x, T = blockDim.x;
     const int row0 = blockIdx.x * R;
     constexpr float LIM = FP8 ? 448.0f : 127.0f;
@@ -174,20 +178,18 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
         const int nw = T >> 6;
 #pragma unroll
         for (int rr = 0; rr < R; rr++) {
-            float amax = 0.0f;
+            float amax = absmax16(v[rr][0]);
 #pragma unroll
-            for (int c = 0; c < P; c++) amax = __builtin_fmaxf(amax, absmax16(v[rr][c]));
-            amax = wave_max_dpp(amax);
-            if ((t & 63) == 0) wave_amax[rr][t >> 6] = amax;
+            for (int c = 1; c < P; c++) amax = __builtin_elementwise_maximum(amax, absmax16(v[rr][c]));
+            const uint32_t bits = wave_max_bits(__float_as_uint(amax));
+            if ((t & 63) == 0) wave_amax[rr][t >> 6] = bits;
         }
         __syncthreads();
 #pragma unroll
         for (int rr = 0; rr < R; rr++) {
-            float amax = wave_amax[rr][0];
-            for (int w = 1; w < nw; w++) {
-                const float b = wave_amax[rr][w];
-                amax = b > amax ? b : amax;
-            }
+            uint32_t bits = wave_amax[rr][0];
+            for (int w = 1; w < nw; w++) bits = max(bits, wave_amax[rr][w]);
+            const float amax = __uint_as_float(bits);
             if (amax == 0.0f) {
                 s[rr] = 1.0f;
                 r[rr] = 1.0f;
@@ -210,7 +212,8 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
             for (int i = 0; i < 4; i++) {
                 if constexpr (FP8) {
                     // gfx950's v_cvt_pk_fp8_f32 is the OCP e4m3fn encode with round to nearest
-                    // even (subnormals included); the clamp keeps it off the overflow path
+                    // even (subnormals included); the clamp keeps it off the overflow path and, as
+                    // in the int8 codes, takes a NaN product to the lower bound
                     float u[4];
 #pragma unroll
                     for (int b = 0; b < 4; b++)

@@ -63,8 +63,16 @@ class Int8Linear(nn.Module):
         tracker = getattr(self, "_ps_tracker", None)
         x = x.float() if safe else x.half()
         out = None
+        finite = False   # out known to be finite
         if not safe and x.device.type == "cuda" and getattr(self, "_ps_native", True):
             out = self._native_forward(x, check=tracker is None)
+            # The kernel path rounds x H to fp16, and |x H| reaches sqrt(g) max|x| where coherent
+            # activations line up with a row of H; the tile path never forms x H.  A non-finite
+            # kernel output is therefore recomputed on the tiles before it is reported or raised.
+            if out is not None:
+                finite = bool(torch.isfinite(out).all())
+                if not finite:
+                    out = None
         if out is None:
             out = torch.empty(x.shape[:-1] + (self.out_features,), dtype=x.dtype, device=x.device)
             prepared = getattr(self, "_ps_prepared", None)
@@ -80,7 +88,7 @@ class Int8Linear(nn.Module):
                 del w
         if tracker is not None:
             tracker.observe(self._ps_finite_slot, out)
-        elif not torch.isfinite(out).all():
+        elif not finite and not torch.isfinite(out).all():
             raise FloatingPointError("NaN/Inf after the INT8 -> FP16 Linear")
         return out
 

@@ -70,6 +70,8 @@ PSQ_API int psq_device_supported(int device);
  *          (the module's input_scale, powershard/quant_linear.py:28-30)
  *   q      [M, K] int8 / e4m3fn codes, row stride ldq bytes
  *   scale  [M] fp32 per-row scale (s = absmax/127 or absmax/448; 0 -> 1)
+ * A row holding a NaN gets a NaN scale (the absmax propagates NaN, as torch's amax does), so its
+ * GEMM output row is NaN; a NaN product takes the lower code bound (-127, or -448 in e4m3).
  * K must be a multiple of 16 and at most 32768.  Bit-exact with the oracle. */
 PSQ_API int psq_quantize_rows_i8(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                          int rot_group, const float *static_scale, int8_t *q, int64_t ldq,
@@ -176,7 +178,8 @@ PSQ_API int psq_dequant_uint4(const uint8_t *wq, const uint16_t *w_scale, const 
                       void *stream);
 
 /* out = round_out((float)q * scale[n]) then, when rot_group > 0, each group of rot_group
- * values multiplied by H^T (= H) with the oracle's fixed-order fast transform, in fp32. */
+ * values multiplied by H^T (= H) with the oracle's fixed-order fast transform, in fp32.
+ * K a multiple of 16, at most 32768. */
 PSQ_API int psq_dequant_i8_rows(const int8_t *q, const float *w_scale, int64_t N, int64_t K,
                         int rot_group, void *out, int out_dtype, void *stream);
 

@@ -37,16 +37,29 @@ LIB_PATH = HERE / "_build" / "libpsq_oracle.so"
 BF16, F16, F32 = 0, 1, 2
 _DT = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
 
-# function -> what pins it (tests/test_oracle_*.py)
+# function -> what pins it (the tests named are in tests/test_oracle_pinning.py)
 PINNING = {
-    "regular_hadamard": "closed form == Kronecker construction (operations.py:72-81); H@H.T == I exactly",
-    "rotate_rows": "== dense x @ H in float64 within fp32 rounding; exact on small-integer inputs",
-    "quantize_rows_i8": "known-answer rows (integer multiples of 2^-e), tie cases, range/absmax invariants",
-    "quantize_rows_fp8": "e4m3 codec exhaustive vs torch float8_e4m3fn; absmax row maps to +-448",
-    "gemm_i8_i32": "== numpy int64 matmul",
-    "epilogue_i32": "within 1 output ulp of float64 acc*a_s*w_s + bias",
-    "gemm_fp8": "== float64 matmul of decoded e4m3 operands",
-    "dequant_uint4": "pack/unpack round trip; == torch restatement; quantize error <= s/2",
+    "regular_hadamard": "closed form == Kronecker construction of operations.py:72-81; H @ H.T == I exactly; "
+                        "not Sylvester (test_hadamard_*)",
+    "rotate_rows": "== dense x @ H in float64 within fp32 rounding; exact on small integers; unit vectors give "
+                   "the rows of H (test_rotation_*)",
+    "quantize_rows_i8": "known-answer rows (integer multiples of 2^-e), ties to even, rotated unit vector, zero "
+                        "row and range invariants, static-scale saturation, NaN-row convention "
+                        "(test_quantize_known_rows_without_rotation, test_quantize_ties_round_to_even, "
+                        "test_quantize_rotated_unit_vector, test_quantize_zero_row_and_invariants, "
+                        "test_quantize_static_scale_saturates, test_quantize_nan_row_convention)",
+    "quantize_rows_fp8": "known-answer rows (e4m3 values x 2^-e, absmax element at +-448: codes and scale 2^-e "
+                         "exact), ties to even (normal and subnormal), static-scale saturation, zero row, torch "
+                         "restatement with torch's own e4m3fn cast (plain and rotated), NaN-row convention "
+                         "(test_quantize_fp8_*, test_quantize_nan_row_convention)",
+    "gemm_i8_i32": "== numpy int64 matmul, also on selected rows; no overflow at the extremes",
+    "epilogue_i32": "within 1 output ulp of float64 acc*a_s*w_s + bias; bf16 output == RNE of the fp32 value",
+    "gemm_fp8": "== float64 matmul of torch-decoded e4m3 operands",
+    "dequant_fp8": "== torch's float8_e4m3fn decode x scale, then torch's cast (per tensor and per row; "
+                   "test_dequant_fp8_matches_torch_decode)",
+    "dequant_uint4": "== the nibble/zero/scale formula on torch tensors; quantize error <= s/2",
+    "dequant_i8_rows": "== dequantize_rows' dense formula (operations.py:84-93) on the test_convrot recipe",
+    "quantize_weight_int8": "round trip through dequantize_rows within half a step per row",
     "gemm_wonly": "== float64 matmul of the dequantized weight",
     "bf16/f16/e4m3 codecs": "exhaustive or dense random vs torch/numpy casts (RNE)",
 }

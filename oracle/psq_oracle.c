@@ -22,6 +22,9 @@
  *    a = max|u|; if a == 0: s = 1, q = 0; else r = 127 / a (fp32 IEEE division, once per
  *    row), s = (a / 127) * 2^-k, q = clamp(rint(u * r), -127, 127), ties to even.
  *    With a static input scale s_in: s = s_in, r = (1 / s_in) * 2^-k.
+ *    NaN: a row holding a NaN has a = NaN (torch's amax propagates NaN), hence s = r = NaN, so
+ *    its dequantized output is NaN wherever the scale reaches it; a NaN product clamps to the
+ *    lower bound, clamp(v) = fmin(fmax(v, -LIM), LIM) with C's fmax/fmin (the non-NaN operand).
  *  - fp8 e4m3fn (OCP) activation quantization per row: the same with 448 in place of 127,
  *    v = clamp(u * r, -448, 448), q = e4m3_rne(v).
  *  - int8 GEMM: acc[m][n] = sum_k a[m][k] * w[n][k] in int32 (exact, order free).
@@ -211,6 +214,38 @@ EXPORT int psq_or_rotate_rows(const void *x, int in_dtype, int64_t M, int64_t K,
     return 0;
 }
 
+/* Row scale of the activation quantizers: r multiplies the (unnormalized) transform output,
+ * s dequantizes the codes.  lim = 127 (int8) or 448 (e4m3); k = log4 of the rotation group. */
+static void row_scale(const float *row, int64_t K, float lim, int k, const float *static_scale, float *r,
+                      float *s)
+{
+    const float post = ldexpf(1.0f, -k);
+    if (static_scale) {
+        *s = static_scale[0];
+        *r = (1.0f / *s) * post;
+        return;
+    }
+    float amax = 0.0f;
+    for (int64_t c = 0; c < K; c++) {
+        const float a = fabsf(row[c]);
+        if (isnan(a)) {
+            amax = a;
+            break;
+        }
+        amax = a > amax ? a : amax;
+    }
+    if (amax == 0.0f) {
+        *s = 1.0f;
+        *r = 1.0f;
+    } else {
+        *r = lim / amax;
+        *s = (amax / lim) * post;
+    }
+}
+
+/* fmin(fmax(v, -lim), lim): C's fmax/fmin return the non-NaN operand, so NaN -> -lim. */
+static inline float clamp_lim(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
+
 /* Per-row int8 quantization of (optionally rotated) activations.
  * q [M, ldq] int8, scale [M] fp32.  static_scale: NULL for dynamic per-row absmax. */
 EXPORT int psq_or_quantize_rows_i8(const void *x, int in_dtype, int64_t M, int64_t K, int64_t ldx,
@@ -233,29 +268,10 @@ EXPORT int psq_or_quantize_rows_i8(const void *x, int in_dtype, int64_t M, int64
             for (int64_t c = 0; c < K; c++) row[c] = load_act(x, m * ldx + c, in_dtype);
             if (g)
                 for (int64_t c = 0; c < K; c += g) fwht4_group(row + c, g, k);
-            float s, r, post = ldexpf(1.0f, -k);
-            if (static_scale) {
-                s = static_scale[0];
-                r = (1.0f / s) * post;
-            } else {
-                float amax = 0.0f;
-                for (int64_t c = 0; c < K; c++) {
-                    float a = fabsf(row[c]);
-                    amax = a > amax ? a : amax;
-                }
-                if (amax == 0.0f) {
-                    s = 1.0f;
-                    r = 1.0f;
-                } else {
-                    r = 127.0f / amax;
-                    s = (amax / 127.0f) * post;
-                }
-            }
-            for (int64_t c = 0; c < K; c++) {
-                float v = rintf(row[c] * r);
-                v = v > 127.0f ? 127.0f : (v < -127.0f ? -127.0f : v);
-                q[m * ldq + c] = (int8_t)v;
-            }
+            float s, r;
+            row_scale(row, K, 127.0f, k, static_scale, &r, &s);
+            for (int64_t c = 0; c < K; c++)
+                q[m * ldq + c] = (int8_t)clamp_lim(rintf(row[c] * r), 127.0f);
             scale[m] = s;
         }
         free(row);
@@ -284,29 +300,9 @@ EXPORT int psq_or_quantize_rows_fp8(const void *x, int in_dtype, int64_t M, int6
             for (int64_t c = 0; c < K; c++) row[c] = load_act(x, m * ldx + c, in_dtype);
             if (g)
                 for (int64_t c = 0; c < K; c += g) fwht4_group(row + c, g, k);
-            float s, r, post = ldexpf(1.0f, -k);
-            if (static_scale) {
-                s = static_scale[0];
-                r = (1.0f / s) * post;
-            } else {
-                float amax = 0.0f;
-                for (int64_t c = 0; c < K; c++) {
-                    float a = fabsf(row[c]);
-                    amax = a > amax ? a : amax;
-                }
-                if (amax == 0.0f) {
-                    s = 1.0f;
-                    r = 1.0f;
-                } else {
-                    r = 448.0f / amax;
-                    s = (amax / 448.0f) * post;
-                }
-            }
-            for (int64_t c = 0; c < K; c++) {
-                float v = row[c] * r;
-                v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
-                q[m * ldq + c] = f32_to_e4m3(v);
-            }
+            float s, r;
+            row_scale(row, K, 448.0f, k, static_scale, &r, &s);
+            for (int64_t c = 0; c < K; c++) q[m * ldq + c] = f32_to_e4m3(clamp_lim(row[c] * r, 448.0f));
             scale[m] = s;
         }
         free(row);

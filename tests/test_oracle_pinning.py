@@ -265,3 +265,119 @@ def test_int8_weight_quantizer_round_trip():
     # rotation is orthonormal: the error norm per row is at most sqrt(K) * s/2
     err = (back - w).norm(dim=1)
     assert torch.all(err <= (512 ** 0.5) * s.squeeze(1) * 0.5 * 1.001)
+
+
+# ------------------------------------------------------------------ fp8 quantize
+def _e4m3_values():
+    """Every finite OCP e4m3fn value (torch's decode of all 256 codes)."""
+    vals = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    return vals[torch.isfinite(vals)]
+
+
+def test_quantize_fp8_known_rows_without_rotation():
+    """x = v * 2^-e with v e4m3-representable and max|v| = 448 -> codes are v's codes (torch's
+    cast) and the scale is 2^-e exactly: r = 448 / amax = 2^e, so u r = v is exact."""
+    g = torch.Generator().manual_seed(31)
+    vals = _e4m3_values()
+    v = vals[torch.randint(0, vals.numel(), (16, 256), generator=g)]
+    v[:, 11] = 448.0
+    v[::2, 11] = -448.0
+    e = torch.arange(16) - 8
+    x64 = v.double() * torch.pow(2.0, -e.double())[:, None]
+    x = x64.to(torch.bfloat16)
+    assert torch.equal(x.double(), x64)           # 4 significant bits: exact in bf16
+    q, s = oracle.quantize_rows_fp8(x)
+    assert torch.equal(q, v.to(torch.float8_e4m3fn).view(torch.uint8))
+    assert torch.equal(s.double(), torch.pow(2.0, -e.double()))
+
+
+def test_quantize_fp8_ties_round_to_even():
+    """scale 1 (absmax 448): midpoints go to the even mantissa, in the normal and subnormal range."""
+    x = torch.tensor([[448.0, 1.0625, 1.1875, -1.0625, -1.1875, 2.0 ** -10, 3 * 2.0 ** -10, 13.0,
+                       15.0, -0.0] + [0.0] * 6], dtype=torch.bfloat16)
+    q, s = oracle.quantize_rows_fp8(x)
+    assert s.item() == 1.0
+    got = q[0, :10].view(torch.float8_e4m3fn).float().tolist()
+    # 1.0625 between 1 (m=0) and 1.125 (m=1) -> 1; 1.1875 between 1.125 (m=1) and 1.25 (m=2) -> 1.25;
+    # 2^-10 between 0 and 2^-9 -> 0; 3 2^-10 between 2^-9 (m=1) and 2^-8 (m=2) -> 2^-8;
+    # 13 between 12 (m=4) and 14 (m=6)... representable (m=5 at [8,16) has step 1): 13 stays;
+    # 15 is 15 (m=7)
+    assert got == [448.0, 1.0, 1.25, -1.0, -1.25, 0.0, 2.0 ** -8, 13.0, 15.0, -0.0]
+
+
+def test_quantize_fp8_static_scale_saturates():
+    x = torch.tensor([[1000.0, -1000.0, 0.25, 0.0] + [0.0] * 12], dtype=torch.bfloat16)
+    q, s = oracle.quantize_rows_fp8(x, static_scale=0.5)
+    assert s.item() == 0.5
+    assert q[0, :4].view(torch.float8_e4m3fn).float().tolist() == [448.0, -448.0, 0.5, 0.0]
+
+
+def test_quantize_fp8_zero_row():
+    x = torch.zeros(3, 64, dtype=torch.bfloat16)
+    x[1, 5] = 2.0
+    q, s = oracle.quantize_rows_fp8(x)
+    assert s[0].item() == 1.0 and s[2].item() == 1.0 and int(q[0].sum()) == 0 and int(q[2].sum()) == 0
+    assert s[1].item() == np.float32(np.float32(2.0) / np.float32(448.0)) and q[1, 5].view(torch.float8_e4m3fn).item() == 448.0
+
+
+@pytest.mark.parametrize("g", [0, 16, 256])
+def test_quantize_fp8_matches_torch_restatement(g):
+    """Per-row absmax (torch amax), r = 448 / a in fp32, clamp, torch's own e4m3fn cast: equal to
+    the oracle's C loop and codec.  The rotated case takes the normalized rotation (pinned above):
+    scaling by 2^-k commutes with the division and the product, so u r and the scale are unchanged."""
+    x = heavy_rows_cpu(24, 2048, seed=40 + g)
+    u = oracle.rotate_rows(x, g) if g else x.float()
+    a = u.abs().amax(1, keepdim=True)
+    r = torch.tensor(448.0) / a
+    codes = (u * r).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    scale = (a / torch.tensor(448.0)).reshape(-1)
+    q, s = oracle.quantize_rows_fp8(x, g)
+    assert torch.equal(q, codes)
+    assert torch.equal(s, scale)
+    # planted mistake: a per-tensor instead of per-row scale is caught
+    wrong = (u * (448.0 / u.abs().max())).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert not torch.equal(q, wrong)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_quantize_nan_row_convention(fp8):
+    """A NaN in a row makes its scale NaN (torch's amax propagates NaN), so the row's dequantized
+    output is NaN; its codes are the lower bound (fmax(NaN, -LIM)); other rows are untouched."""
+    x = heavy_rows_cpu(4, 512, seed=5)
+    x[2, 100] = float("nan")
+    fn = oracle.quantize_rows_fp8 if fp8 else oracle.quantize_rows_i8
+    for g in (0, 256):
+        q, s = fn(x, g)
+        assert torch.isnan(s[2]) and not torch.isnan(s[[0, 1, 3]]).any()
+        assert torch.isnan(x.float()[2].abs().amax())            # torch's convention
+        low = torch.full((512,), 0xFE, dtype=torch.uint8) if fp8 else torch.full((512,), -127, dtype=torch.int8)
+        assert torch.equal(q[2], low)
+        clean = x.clone()
+        clean[2] = 0
+        qc, sc = fn(clean, g)
+        assert torch.equal(q[[0, 1, 3]], qc[[0, 1, 3]]) and torch.equal(s[[0, 1, 3]], sc[[0, 1, 3]])
+
+
+# -------------------------------------------------------------------- fp8 decode
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_dequant_fp8_matches_torch_decode(per_row, out_dtype):
+    """round_out(e4m3(q) * s): torch's float8_e4m3fn decode times the fp32 scale, then torch's cast."""
+    g = torch.Generator().manual_seed(41)
+    codes = torch.randint(0, 256, (37, 96), generator=g, dtype=torch.uint8)
+    codes[codes == 0x7F] = 0x7E
+    codes[codes == 0xFF] = 0xFE
+    s = torch.rand(37, generator=g) * 1e-2 + 1e-4 if per_row else torch.tensor(3.1e-3)
+    got = oracle.dequant_fp8(codes, s, out_dtype)
+    ref = (codes.view(torch.float8_e4m3fn).float() * (s[:, None] if per_row else s)).to(out_dtype)
+    assert torch.equal(got.view(torch.int16) if out_dtype != torch.float32 else got,
+                       ref.view(torch.int16) if out_dtype != torch.float32 else ref)
+
+
+def heavy_rows_cpu(M, K, seed):
+    """N(0,1) rows with 1% of channels x20, bf16 (the activation recipe of the GPU tests)."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=gen)
+    idx = torch.randperm(K, generator=gen)[: max(1, K // 100)]
+    x[:, idx] *= 20
+    return x.to(torch.bfloat16)

@@ -1,0 +1,281 @@
+"""GPU parity cases beyond the per-kernel suite: the reference's own QuantLinear criterion, the
+weight-only kernels at the c2 text-encoder shape (their 256-row tile instantiation), the on-disk
+int8 ConvRot module through the kernels, NaN rows, and the dequantize kernels at K = 25600.
+
+* ``test_native_matches_dequantize_branch``: the reference checks QuantLinear against
+  F.linear(x, qt.dequantize()) (tests/test_quant_formats_torch.py:80-103).  W4A16 quantizes no
+  activations, so the native output meets 1e-2 rms of that directly (or differs by one bf16 ulp, a
+  rounding tie of two fp32 sums).  W8A8 and FP8 quantize the activations per token, so their
+  difference from the dequantize branch is the activation quantization error; it is checked against
+  the bound that error allows, computed in float64 per output (no oracle involved):
+  sum_k |dx_k| |w_k| with |dx_k| <= s_a / 2 (int8 codes) or 2^-4 |x_k| + 2^-10 s_a (e4m3), plus the
+  bf16 rounding of the dequantized weight (2^-8 relative) and of both outputs (half an ulp each).
+"""
+import json
+import os
+
+import pytest
+import torch
+from torch import nn
+
+import oracle
+from conftest import heavy_rows, seeded
+from test_gpu_kernels import assert_bitexact, assert_fp32_path
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _layer(K, N, weight_format, opts, dev, seed, compute="native", dtype=torch.bfloat16):
+    from powershard_amd.quant_linear import install_quant_linears, quantized_from_float, pack
+    net = nn.Sequential(nn.Linear(K, N)).to(dtype)
+    tensors = {"0.weight": {"key": "0.weight", "dtype": "BF16", "shape": [N, K]}}
+    install_quant_linears(net, tensors, weight_format, compute, None, dtype, dev, quant_options=opts)
+    layer = net[0]
+    g = seeded(seed)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    qt = quantized_from_float(w, layer._ps_qplan.fmt, **opts)
+    layer.qbytes = nn.Parameter(pack(qt, layer._ps_qplan, dev), requires_grad=False)
+    b = (torch.randn(N, generator=g) * 0.05).to(dtype)
+    layer.bias = nn.Parameter(b.to(dev), requires_grad=False)
+    return layer, qt, b
+
+
+def _ulp_bf16(v):
+    return torch.pow(2.0, torch.floor(torch.log2(v.abs().clamp(min=2.0 ** -126))) - 7)
+
+
+# ------------------------------------------------- the reference's QuantLinear criterion
+@pytest.mark.parametrize("weight_format,opts", [("int8", {"convrot": True, "convrot_groupsize": 256}),
+                                                ("int8", {"convrot": False}), ("fp8", {}),
+                                                ("int4", {"group_size": 128})])
+def test_native_matches_dequantize_branch(gpu, weight_format, opts):
+    K, N, M = 1024, 512, 300
+    layer, qt, b = _layer(K, N, weight_format, opts, gpu, seed=61)
+    x = heavy_rows(M, K, seed=62)
+    with torch.no_grad():
+        y = layer(x.to(gpu)).float().cpu()
+        wd = qt.dequantize().to(torch.bfloat16)                              # the dequantize branch's weight
+        ref = torch.nn.functional.linear(x.to(gpu), wd.to(gpu), b.to(gpu)).float().cpu()
+    assert layer._ps_native
+    err = (y - ref).abs()
+    rms = ref.pow(2).mean().sqrt().item()
+    print(f"{weight_format} {opts}: max|native - dequantize branch| = {err.max().item():.3e}, "
+          f"rms err / rms = {(err.pow(2).mean().sqrt() / rms).item():.3e}")
+    if weight_format == "int4":
+        bound = torch.maximum(torch.full_like(ref, 1e-2 * rms), _ulp_bf16(ref))
+    else:
+        w64 = qt.dequantize().double().cpu()              # exact dequantized weight (rotated back)
+        x64 = x.double()
+        if weight_format == "int8":
+            g = opts["convrot_groupsize"] if opts.get("convrot") else 0
+            _, sa = oracle.quantize_rows_i8(x, g)
+            # codes are of u = x H (or x); |du| <= s_a / 2 per element, and with the stored weight
+            # q s (= W H) the error of the product is sum_k |du_k| |(q s)_nk|
+            ws = (qt._qdata.double() * qt._params.scale.double()).cpu()
+            act = sa.double()[:, None] / 2 * ws.abs().sum(1)[None, :]
+        else:
+            _, sa = oracle.quantize_rows_fp8(x)
+            dx = 2.0 ** -4 * x64.abs() + 2.0 ** -10 * sa.double()[:, None]
+            act = dx @ w64.abs().T
+        wround = 2.0 ** -8 * (x64.abs() @ w64.abs().T)   # bf16 rounding of the dequantized weight
+        acc = K * 2.0 ** -22 * (x64.abs() @ w64.abs().T)  # fp32 accumulation, both paths
+        bound = act + wround + acc + (_ulp_bf16(y.double()) + _ulp_bf16(ref.double())) / 2
+    bad = err.double() > bound
+    assert not bad.any(), f"{int(bad.sum())} outputs exceed the bound; worst excess {(err.double() - bound).max():.3e}"
+
+
+# ------------------------------------------------------- NaN rows (torch's amax convention)
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("g", [0, 256])
+def test_quantize_nan_row(gpu, fp8, g):
+    """A NaN makes its row's scale NaN (codes: the lower bound); other rows are unchanged."""
+    from powershard_amd import ops
+    x = heavy_rows(6, 1024, seed=63)
+    x[3, 77] = float("nan")
+    q, s = ops.quantize_rows(x.to(gpu), fp8=fp8, rot_group=g)
+    rq, rs = (oracle.quantize_rows_fp8 if fp8 else oracle.quantize_rows_i8)(x, g)
+    assert_bitexact(q.view(torch.uint8) if fp8 else q, rq, "codes")
+    s = s.cpu()
+    assert torch.isnan(s[3]) and torch.isnan(rs[3])
+    keep = [0, 1, 2, 4, 5]
+    assert_bitexact(s[keep], rs[keep], "scales of the other rows")
+
+
+@pytest.mark.parametrize("weight_format,opts", [("int8", {"convrot": True, "convrot_groupsize": 256}), ("fp8", {})])
+def test_quantlinear_nan_row_propagates(gpu, weight_format, opts):
+    """The finite tracker sees a NaN input row as a NaN output row, as with F.linear."""
+    layer, _, _ = _layer(512, 256, weight_format, opts, gpu, seed=64)
+    x = heavy_rows(8, 512, seed=65)
+    x[5, 300] = float("nan")
+    with torch.no_grad():
+        y = layer(x.to(gpu)).float().cpu()
+    assert torch.isnan(y[5]).all()
+    assert torch.isfinite(y[[0, 1, 2, 3, 4, 6, 7]]).all()
+
+
+# ------------------------------------------ weight-only GEMMs at the c2 shape (256-row tiles)
+def _wonly_rows(x, wd, b, rows):
+    return oracle.gemm_wonly(x, wd, None, b, out_dtype=torch.float32, row_ids=rows)
+
+
+def _sample_rows(M, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    mid = torch.randperm(M - 64, generator=g)[: n - 64] + 32
+    return torch.cat([torch.arange(32), mid.sort().values, torch.arange(M - 32, M)])
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N", [25600, 25664])
+def test_gemm_w4a16_256_row_tiles(gpu, xdt, N):
+    """M = 512 with N >= 25600 has more 128-row tiles (4 x 100) than CUs, so the tiled kernel runs its
+    256-row instantiation (its own ring depth and LDS layout); N = 25664 adds a partial column tile.
+    K = 512 keeps the oracle quick; every row of a 128-row sample is checked."""
+    from powershard_amd import ops
+    M, K, gs = 512, 512, 128
+    x = heavy_rows(M, K, seed=66, outlier_frac=0, dtype=xdt)
+    w = torch.randn(N, K, generator=seeded(67)) * 0.02
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    b = (torch.randn(N, generator=seeded(68)) * 0.01).to(xdt)
+    args = (x.to(gpu), wq.to(gpu), s.to(gpu), z.to(gpu), gs, b.to(gpu))
+    rows = _sample_rows(M, 128, 69)
+    y32 = ops.gemm_w4a16(*args, out_dtype=torch.float32).cpu()[rows]
+    yb = ops.gemm_w4a16(*args, out_dtype=torch.bfloat16).cpu()[rows]
+    wd = oracle.dequant_uint4(wq, s, z, gs, out_dtype=xdt)
+    assert_fp32_path(y32, yb, _wonly_rows(x, wd, b, rows), f"w4a16 256-row tiles N={N}")
+
+
+@pytest.mark.parametrize("N", [16640, 16400])
+def test_gemm_w8a16_256_row_tiles(gpu, N):
+    """W8A16 at M = 512 with 4 x 65 128-row tiles (> 256 CUs): the 256-row instantiation."""
+    from powershard_amd import ops
+    M, K = 512, 640
+    x = heavy_rows(M, K, seed=70, outlier_frac=0)
+    w = torch.randn(N, K, generator=seeded(71)) * 0.02
+    q, s = oracle.quantize_weight_int8(w, False)
+    b = (torch.randn(N, generator=seeded(72)) * 0.01).to(torch.bfloat16)
+    args = (x.to(gpu), q.to(gpu), s.to(gpu), b.to(gpu))
+    rows = _sample_rows(M, 128, 73)
+    y32 = ops.gemm_w8a16(*args, out_dtype=torch.float32).cpu()[rows]
+    yb = ops.gemm_w8a16(*args, out_dtype=torch.bfloat16).cpu()[rows]
+    ref = oracle.gemm_wonly(x, q.to(torch.bfloat16), s, b, out_dtype=torch.float32, row_ids=rows)
+    assert_fp32_path(y32, yb, ref, f"w8a16 256-row tiles N={N}")
+
+
+def test_c2_int4_text_encoder_mlp(gpu):
+    """The c2 workload itself: uint4 g128 weights 25600 x 5120, M = 512 prompt tokens, through the
+    QuantLinear module; 256 sampled rows x all 25600 columns against the oracle."""
+    from powershard_amd import ops
+    M, K, N = 512, 5120, 25600
+    layer, qt, b = _layer(K, N, "int4", {"group_size": 128}, gpu, seed=74)
+    x = heavy_rows(M, K, seed=75, outlier_frac=0)
+    with torch.no_grad():
+        yb = layer(x.to(gpu)).cpu()
+        p = qt._params
+        y32 = ops.gemm_w4a16(x.to(gpu), qt._qdata.to(gpu), p.scale.to(gpu), p.zero.to(gpu), p.group_size,
+                             layer.bias, out_dtype=torch.float32).cpu()
+    assert layer._ps_native
+    rows = _sample_rows(M, 256, 76)
+    wd = oracle.dequant_uint4(qt._qdata, p.scale, p.zero, 128, out_dtype=torch.bfloat16)
+    ref = _wonly_rows(x, wd, b, rows)
+    assert_fp32_path(y32[rows], yb[rows], ref, "c2 W4A16 512x5120->25600")
+
+
+# ----------------------------------------------- on-disk int8 ConvRot module (comfy_quant)
+def test_file_int8_convrot_module_native_bitexact(gpu, tmp_path):
+    """An int8_tensorwise ConvRot module as the reference's checkpoints store it -- I8 [N, K] weight,
+    F32 [N, 1] weight_scale and the 72-byte comfy_quant payload of models/convrot_config.json --
+    loaded with weight_format="as_file" and compute="native", packed by build_bytes onto the GPU,
+    and run through the kernels: bit-exact with the oracle's quantized forward
+    (powershard/checkpoint.py:63-82, quant_linear.py:407-444)."""
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+    from powershard_amd import quant_formats as qf
+    from powershard_amd import quant_linear as ql
+    raw = open(os.path.join(GOLDEN, "convrot_config.json"), "rb").read().strip()
+    conf = json.loads(raw)
+    N, K = 768, 5376                                       # H3 width (21 ConvRot groups)
+    w = torch.randn(N, K, generator=seeded(77)) * 0.02
+    q, s = oracle.quantize_weight_int8(w, True, 256)
+    bias = (torch.randn(N, generator=seeded(78)) * 0.01).to(torch.bfloat16)
+    path = tmp_path / "h3_fc.safetensors"
+    save_file({"blk.fc.weight": q, "blk.fc.weight_scale": s.float(), "blk.fc.bias": bias,
+               "blk.fc.comfy_quant": torch.frombuffer(bytearray(raw), dtype=torch.uint8)}, str(path))
+    code = {torch.float32: "F32", torch.bfloat16: "BF16", torch.int8: "I8", torch.uint8: "U8"}
+    with safe_open(str(path), framework="pt") as f:
+        table = {k: {"key": k, "dtype": code[f.get_tensor(k).dtype], "shape": list(f.get_tensor(k).shape)}
+                 for k in f.keys()}
+        qf.annotate_quantized(table, lambda n: json.loads(bytes(f.get_tensor(n).tolist())))
+    assert table["blk.fc.weight"]["comfy_quant"] == conf
+    net = nn.ModuleDict({"blk": nn.ModuleDict({"fc": nn.Linear(K, N).to(torch.bfloat16)})})
+    report = ql.install_quant_linears(net, table, "as_file", "native", None, torch.bfloat16, gpu)
+    layer = net["blk"]["fc"]
+    assert report["modules"]["int8_tensorwise"]["source"] == {"file": 1}
+    with safe_open(str(path), framework="pt") as f:
+        full, used = ql.build_bytes(layer, f, gpu)
+    assert used == {"blk.fc.weight", "blk.fc.weight_scale", "blk.fc.comfy_quant"}
+    assert full.device.type == "cuda"
+    layer.qbytes = nn.Parameter(full, requires_grad=False)
+    layer.bias = nn.Parameter(bias.to(gpu), requires_grad=False)
+    x = heavy_rows(96, K, seed=79)
+    with torch.no_grad():
+        y = layer(x.to(gpu))
+    assert layer._ps_native
+    qa, sa = oracle.quantize_rows_i8(x, 256)
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, q), sa, s, bias)
+    assert_bitexact(y, ref, "as_file int8 ConvRot module")
+
+
+# ------------------------------------------------------------ dequantize at K = 25600
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_dequant_i8_rows_k25600(gpu, out_dtype):
+    """Qwen3-VL down_proj width: two 16-value chunks per thread."""
+    from powershard_amd import ops
+    gen = seeded(80)
+    q = torch.randint(-127, 128, (9, 25600), generator=gen, dtype=torch.int8)
+    s = torch.rand(9, 1, generator=gen) * 1e-3
+    for g in (0, 256, 1024):
+        got = ops.dequant_i8_rows(q.to(gpu), s.to(gpu), g, out_dtype)
+        assert_bitexact(got, oracle.dequant_i8_rows(q, s, g, out_dtype), f"int8 row dequant K=25600 g={g}")
+
+
+def test_quantlinear_dequantize_mode_k25600(gpu):
+    """compute="dequantize" at K = 25600 runs the row dequantization kernel (ConvRot inverse)."""
+    layer, qt, b = _layer(25600, 64, "int8", {"convrot": True, "convrot_groupsize": 256}, gpu, seed=81,
+                          compute="dequantize")
+    x = heavy_rows(5, 25600, seed=82)
+    with torch.no_grad():
+        y = layer(x.to(gpu)).cpu()
+    wd = oracle.dequant_i8_rows(qt._qdata, qt._params.scale, 256, torch.bfloat16)
+    ref = torch.nn.functional.linear(x.to(gpu), wd.to(gpu), b.to(gpu)).cpu()
+    assert_bitexact(y, ref, "dequantize mode at K=25600")
+
+
+# ------------------------------------------------------ Int8Linear with coherent activations
+def test_int8linear_coherent_activations_stay_finite(gpu):
+    """Activations aligned with a row of H make |x H| = sqrt(g) max|x| (80000 here), beyond fp16: the
+    kernel path's rotation overflows, the layer recomputes the call on the row tiles, and the output
+    equals the reference tile path's (finite, as the reference's is)."""
+    from powershard_amd.operations import Int8Linear
+    K, N, g = 512, 64, 256
+    gen = seeded(83)
+
+    def make():
+        lin = Int8Linear(torch.nn.Linear(K, N), dict(convrot=True, group_size=g), rows=32).to_empty(device=gpu)
+        w = torch.randn(N, K, generator=seeded(84)) * 0.02
+        q, s = oracle.quantize_weight_int8(w, True, g)
+        lin.weight.data.copy_(q)
+        lin.weight_scale.data.copy_(s)
+        lin.bias = torch.nn.Parameter(torch.zeros(N, dtype=torch.float16, device=gpu), requires_grad=False)
+        return lin
+    h = oracle.regular_hadamard(g)
+    x = torch.randn(4, K, generator=gen).half()
+    x[1, :g] = (5000 * 16 * h[7]).half()          # entries +-5000: x H = 80000 e_7 in that group
+    kern, tiles = make(), make()
+    tiles._ps_native = False
+    with torch.no_grad():
+        y = kern(x.to(gpu))
+        ref = tiles(x.to(gpu))
+    assert torch.isfinite(y).all()
+    assert_bitexact(y, ref, "Int8Linear recomputed on the tiles")
