@@ -9,19 +9,24 @@ y [32760, 13824] bf16.  A step is one forward of the module (both kernels); `val
 2*M*N*K / step time in TOPS with all inputs resident in HBM.
 
 `roofline` is the int8 GEMM kernel (the dominant one): algorithmic ops per launch divided by
-its average launch time, timed with HIP events around each launch on its stream during the
-timed steps.  `cpu_baseline` is the CPU oracle (the quantized-reference restatement in C with
-OpenMP) on a bounded sample of rows of the same workload, on this host's cores.
+its average launch time, timed with HIP events on its stream around a loop of back-to-back
+launches on the headline's quantized input.  `cpu_baseline` is the reference's own CPU path for
+the same layer -- QuantLinear's dequantize branch: dequantize_rows (q * s, ConvRot inverse) and
+F.linear in bf16 on torch-CPU (powershard/quant_linear.py:219-220, operations.py:84-93) -- on a
+bounded row sample, on all of this process's CPU threads and on one, with the c0 / c2 layers and
+one Wan-14B block (x40, derived) beside it and the C oracle's quantized forward as a second figure.
 
-`extra` carries the other shapes: the int4 (W4A16) text-encoder MLP at M=512 with an M sweep,
-the fp8 QKV projection, the int8 weight-only layer, the Wan-14B FFN with its GELU in the
-up-projection's epilogue against the unfused reference sequence, the MiniMax-H3 MLP with its SiLU
-gate in fc1's epilogue (fp16, M=8192) against its reference sequence, the 8-way token shard's
-per-GPU share (M=4095), and the 40-block Wan-14B linear stack.
+`extra` carries the other shapes, each with a sampled-row check against the oracle: the int4
+(W4A16) text-encoder MLP at M=512 with an M sweep, the fp8 QKV projection, the int8 weight-only
+layer, the Wan-14B FFN with its GELU in the up-projection's epilogue against the unfused reference
+sequence, the MiniMax-H3 MLP with its SiLU gate in fc1's epilogue (fp16, M=8192) against its
+reference sequence, the 8-way token shard's per-GPU share (M=4095), and the 40-block Wan-14B
+linear stack.
 """
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 
@@ -53,7 +58,8 @@ def parse():
                     "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, h3_mlp_silu_gate, shard_m4095, wan14b_stack); "
                     "default all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU baseline sample time")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="target time of each timed CPU baseline sample (about ten samples in all)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain elementwise copy of 1 GiB (3 launches), the reference point that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -160,6 +166,7 @@ def untimed_kernel_ms(step, steps, warmup):
 # -------------------------------------------------------------------- workloads
 def headline(args):
     import torch
+    from powershard_amd import ops
     M, K, N = 32760, 5120, 13824
     sid = 1
     log(f"[bench] headline W8A8+ConvRot M={M} K={K} N={N}: building inputs")
@@ -174,29 +181,39 @@ def headline(args):
     def step():
         with torch.no_grad():
             layer(x)
-    ms, per = timed_steps(step, args.steps, args.warmup)
-    ms_clean = untimed_kernel_ms(step, args.steps, 2)
+    ms = untimed_kernel_ms(step, args.steps, args.warmup)
+    # each kernel alone, back to back on the same stream: events around the loop, not per launch
+    qx, sx = ops.quantize_rows(x, rot_group=256)
+    wq, ws = qt._qdata, qt._params.scale
+    gemm_ms = untimed_kernel_ms(lambda: ops.gemm_i8(qx, sx, wq, ws, b), args.steps, 3)
+    quant_ms = untimed_kernel_ms(lambda: ops.quantize_rows(x, rot_group=256), args.steps, 3)
     ops_per_step = 2.0 * M * N * K
-    gemm_ms = per["gemm_i8"]
-    quant_ms = per["quantize_rows_i8"]
-    tops = ops_per_step / (ms_clean * 1e-3) / 1e12
+    tops = ops_per_step / (ms * 1e-3) / 1e12
     gemm_tops = ops_per_step / (gemm_ms * 1e-3) / 1e12
     quant_bytes = M * K * 2 + M * K + M * 4
-    res = dict(M=M, N=N, K=K, ms_per_step=ms_clean, ms_per_step_with_events=ms, tops=tops, gemm_ms=gemm_ms,
-               gemm_tops=gemm_tops, quant_ms=quant_ms, quant_gbs=quant_bytes / (quant_ms * 1e-3) / 1e9,
-               quant_bytes=quant_bytes)
-    log(f"[bench] headline: {ms_clean:.3f} ms/step, {tops:.1f} TOPS; gemm {gemm_ms:.3f} ms = {gemm_tops:.1f} TOPS "
+    res = dict(M=M, N=N, K=K, ms_per_step=ms, tops=tops, gemm_ms=gemm_ms, gemm_tops=gemm_tops, quant_ms=quant_ms,
+               quant_gbs=quant_bytes / (quant_ms * 1e-3) / 1e9, quant_bytes=quant_bytes)
+    log(f"[bench] headline: {ms:.3f} ms/step, {tops:.1f} TOPS; gemm {gemm_ms:.3f} ms = {gemm_tops:.1f} TOPS "
         f"({100 * gemm_tops / PEAK_INT8_TOPS:.1f}% of int8 peak); quant {quant_ms * 1e3:.1f} us = "
         f"{res['quant_gbs']:.0f} GB/s")
     # parity rows: the first 64, 128 spread over the middle, and the last 64 (the partial last tile)
-    g = torch.Generator().manual_seed(5000 + sid)
-    mid = torch.randperm(M - 128, generator=g)[:128] + 64
-    idx = torch.cat([torch.arange(64), mid.sort().values, torch.arange(M - 64, M)])
-    sample = dict(x=x[:8192].cpu(), qdata=qt._qdata.cpu(), scale=qt._params.scale.cpu(), bias=b.cpu(),
-                  rows=idx, x_rows=x[idx.to(x.device)].cpu(), y_rows=y[idx.to(y.device)].cpu())
-    del layer, qt, x, y
+    idx = sample_rows(M, 256, 5000 + sid)
+    sample = dict(x=x[:4096].cpu(), qdata=qt._qdata.cpu(), scale=qt._params.scale.cpu(), bias=b.cpu(),
+                  rows=idx, x_rows=x[idx.to(x.device)].cpu(), y_rows=y[idx.to(y.device)].cpu(), M=M)
+    del layer, qt, x, y, qx, sx
     torch.cuda.empty_cache()
     return res, sample
+
+
+def sample_rows(M, n, seed):
+    """n row indices: the first and last quarter-n rows (the edge tiles) and the rest spread between."""
+    import torch
+    if M <= n:
+        return torch.arange(M)
+    e = n // 4
+    g = torch.Generator().manual_seed(seed)
+    mid = torch.randperm(M - 2 * e, generator=g)[: n - 2 * e] + e
+    return torch.cat([torch.arange(e), mid.sort().values, torch.arange(M - e, M)])
 
 
 def check_headline_parity(sample):
@@ -211,6 +228,18 @@ def check_headline_parity(sample):
     err = (got.float() - ref.float()).abs().max().item()
     rms = ref.float().pow(2).mean().sqrt().item()
     return dict(rows_checked=int(sample["rows"].numel()), bitexact=same, max_abs_err_over_rms=err / rms)
+
+
+def within_bar(got, ref):
+    """Sampled-row check of an fp32-accumulating path: every element within max(1e-2 rms, one bf16
+    ulp of the reference value) -- the ulp covers rounding ties of two fp32 sums at large |y|."""
+    import torch
+    got, ref = got.float(), ref.float()
+    rms = ref.pow(2).mean().sqrt()
+    err = (got - ref).abs()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(ref.abs().clamp(min=1e-30))) - 7)
+    return dict(rows_checked=int(got.shape[0]), within_bar=bool((err <= torch.maximum(1e-2 * rms, ulp)).all()),
+                max_abs_err_over_rms=(err.max() / rms).item())
 
 
 PROFILE = os.path.join(ROOT, "profiles", "gemm_i8_w8a8_convrot_m32760_n13824_k5120.md")
@@ -231,46 +260,171 @@ def profiled_traffic():
         return None
 
 
-def cpu_baseline(sample, target_s):
-    """Oracle (C, OpenMP, all affinity cores) W8A8 forward on a bounded row sample."""
+# ------------------------------------------------------------------ CPU baseline
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _seconds(fn):
+    t0 = time.perf_counter()
+    out = fn()
+    return time.perf_counter() - t0, out
+
+
+def reference_cpu_forward(dequant, x_rows, M, bias, target_s):
+    """Time the reference's dequantize-branch forward on the CPU: the per-call dequantization of
+    the whole weight (independent of M) and the bf16 F.linear on a row sample grown until it takes
+    about target_s / 3; the M-row forward is projected as t_dequant + t_linear * M / rows."""
+    import torch
+    t_deq, w = _seconds(dequant)
+    N, K = w.shape
+    torch.nn.functional.linear(x_rows[:4], w, bias)          # kernel selection / first-call work
+    rows = 4
+    while True:
+        t_lin, _ = _seconds(lambda: torch.nn.functional.linear(x_rows[:rows], w, bias))
+        if t_lin * 3 > target_s or rows >= min(M, x_rows.shape[0]):
+            break
+        rows = min(rows * 4, M, x_rows.shape[0])
+    t_full = t_deq + t_lin * M / rows
+    return dict(tops=2.0 * M * N * K / t_full / 1e12, forward_s=t_full, dequant_s=t_deq, linear_rows=rows,
+                linear_s=t_lin)
+
+
+def _convrot_dequant(q, s, g):
+    import oracle
+    import torch
+    return lambda: oracle.dequantize_rows(q, s, g > 0, g, torch.bfloat16)
+
+
+def _rowwise_dequant(q, s):
+    import torch
+    return lambda: (q.float() * s.float().reshape(-1, 1)).to(torch.bfloat16)
+
+
+def _uint4_dequant(wq, s, z, g):
+    """w = (q - z) s per (row, group), low nibble = even k, then bf16: torch ops on the CPU."""
+    import torch
+
+    def run():
+        q = torch.stack([wq & 15, wq >> 4], -1).reshape(wq.shape[0], -1).float()
+        zz = z.float().repeat_interleave(g, 1)
+        ss = s.float().repeat_interleave(g, 1)
+        return ((q - zz) * ss).to(torch.bfloat16)
+    return run
+
+
+def cpu_inputs(sample):
+    """CPU copies of the c0, c2 and one-Wan-block (c4) layers, built on the GPU with the seeds of
+    their GPU workloads, and their activation rows."""
+    import torch
+    c = {}
+    layer, qt, b = quant_layer(5120, 5120, "int8", 0)
+    c["c0"] = dict(q=qt._qdata.cpu(), s=qt._params.scale.cpu(), b=b.cpu(),
+                   x=activations(1024, 5120, 0, outlier_scale=1.0).cpu())
+    layer, qt, b = quant_layer(5120, 25600, "int4", 2, seed=1002, opts={"group_size": 128})
+    p = qt._params
+    c["c2"] = dict(q=qt._qdata.cpu(), s=p.scale.cpu(), z=p.zero.cpu(), b=b.cpu(),
+                   x=activations(512, 5120, 2, outlier_scale=1.0).cpu())
+    opts = {"convrot": True, "convrot_groupsize": 256}
+    blk = []
+    for i, (k_, n_) in enumerate(((5120, 5120),) * 4 + ((5120, 13824), (13824, 5120))):
+        layer, qt, b = quant_layer(k_, n_, "int8", 4, seed=1004 + i + 1, opts=opts)
+        blk.append(dict(q=qt._qdata.cpu(), s=qt._params.scale.cpu(), b=b.cpu()))
+    c["c4"] = dict(layers=blk, x=activations(256, 5120, 4, outlier_scale=50.0, student_t=True).cpu(),
+                   h=activations(256, 13824, 104, outlier_scale=50.0, student_t=True).cpu())
+    del layer, qt
+    torch.cuda.empty_cache()
+    return c
+
+
+def cpu_baseline(sample, inputs, target_s):
+    """The reference's CPU path (QuantLinear dequantize branch on torch-CPU) for the headline layer on
+    all threads and on one, the c0 / c2 layers and one Wan-14B block (x40, derived), and the C
+    oracle's quantized W8A8 forward as a second figure."""
     import torch
     import oracle
-    N, K = sample["qdata"].shape
-    threads = oracle.num_threads()
-    x = sample["x"]
+    threads = torch.get_num_threads()
+    M, (N, K) = sample["M"], sample["qdata"].shape
+    q, s, b, x = sample["qdata"], sample["scale"], sample["bias"], sample["x"]
+    head = reference_cpu_forward(_convrot_dequant(q, s, 256), x, M, b, target_s)
+    log(f"[bench] cpu reference path, {threads} threads: {head['tops'] * 1e3:.1f} GOPS (dequant "
+        f"{head['dequant_s']:.2f} s, linear {head['linear_rows']} rows {head['linear_s']:.2f} s)")
+    torch.set_num_threads(1)
+    try:
+        one = reference_cpu_forward(_convrot_dequant(q, s, 256), x, M, b, target_s)
+    finally:
+        torch.set_num_threads(threads)
+    log(f"[bench] cpu reference path, 1 thread: {one['tops'] * 1e3:.1f} GOPS")
+    configs = {}
+    c0 = inputs["c0"]
+    configs["c0_int8_weight_only_1024x5120x5120"] = reference_cpu_forward(
+        _rowwise_dequant(c0["q"], c0["s"]), c0["x"], 1024, c0["b"], target_s)
+    c2 = inputs["c2"]
+    configs["c2_uint4_g128_512x5120x25600"] = reference_cpu_forward(
+        _uint4_dequant(c2["q"], c2["s"], c2["z"], 128), c2["x"], 512, c2["b"], target_s)
+    c4 = inputs["c4"]
+    block_s, block_ops = 0.0, 0.0
+    for i, lay in enumerate(c4["layers"]):
+        xr = c4["h"] if i == 5 else c4["x"]
+        r = reference_cpu_forward(_convrot_dequant(lay["q"], lay["s"], 256), xr, 32760, lay["b"], target_s / 3)
+        block_s += r["forward_s"]
+        block_ops += 2.0 * 32760 * lay["q"].shape[0] * lay["q"].shape[1]
+    configs["c4_wan14b_40_blocks_derived"] = dict(block_s=block_s, total_s=40 * block_s,
+                                                  tops=block_ops / block_s / 1e12,
+                                                  note="one block timed (6 layers, row samples), x40")
+    for k, v in configs.items():
+        log(f"[bench] cpu reference path {k}: {v['tops'] * 1e3:.1f} GOPS")
+    # the oracle's quantized forward (rotate + quantize, int32 GEMM, epilogue) in C with OpenMP
+    def oracle_forward(rows):
+        qa, sa = oracle.quantize_rows_i8(x[:rows], 256)
+        return oracle.epilogue_i32(oracle.gemm_i8_i32(qa, q), sa, s, b)
     rows = 8
     while True:
-        t0 = time.perf_counter()
-        qa, sa = oracle.quantize_rows_i8(x[:rows], 256)
-        y = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, sample["qdata"]), sa, sample["scale"], sample["bias"])
-        dt = time.perf_counter() - t0
-        if dt * 4 > target_s or rows >= x.shape[0]:
+        t, _ = _seconds(lambda: oracle_forward(rows))
+        if t * 3 > target_s or rows >= x.shape[0]:
             break
         rows = min(x.shape[0], rows * 4)
-    del y
-    tops = 2.0 * rows * N * K / dt / 1e12
-    return dict(value=tops, unit="TOPS", cores=threads, kind="port",
-                sample=f"W8A8+ConvRot forward (rotate+quantize, int32 GEMM, epilogue) of {rows} token rows x "
-                       f"{N}x{K} weights, {dt:.2f} s on {threads} threads; same synthetic inputs as the GPU run")
+    orc = dict(tops=2.0 * rows * N * K / t / 1e12, rows=rows, seconds=t, threads=oracle.num_threads())
+    return dict(value=head["tops"], unit="TOPS", cores=threads, kind="port", cpu_model=cpu_model(),
+                algorithm="the reference's CPU path: dequantize_rows (q*s, ConvRot inverse) + bf16 F.linear "
+                          "(powershard/quant_linear.py:219-220, operations.py:84-93) on torch-CPU",
+                sample=f"headline layer {M}x{K}->{N}: dequantization of the whole weight timed once "
+                       f"({head['dequant_s']:.2f} s), F.linear on {head['linear_rows']} rows "
+                       f"({head['linear_s']:.2f} s), projected to M={M}; same synthetic inputs as the GPU run",
+                detail=head, single_thread=dict(value=one["tops"], unit="TOPS", detail=one), configs=configs,
+                oracle_w8a8=dict(value=orc["tops"], unit="TOPS", rows=orc["rows"], seconds=orc["seconds"],
+                                 threads=orc["threads"],
+                                 note="C oracle: rotate+quantize, int32 GEMM, epilogue (the quantized reference)"))
 
 
 def extra_int4(args):
-    """W4A16 uint4 g128 Qwen3-VL-32B text-encoder MLP, K=5120 -> N=25600; M sweep; MALL-defeating
-    rotation over 4 distinct weight copies (4 x 69.6 MB > 256 MB Infinity Cache)."""
+    """W4A16 uint4 g128 Qwen3-VL-32B text-encoder MLP, K=5120 -> N=25600; M sweep.  Weights rotate
+    over 12 distinct copies (12 x 69.6 MB = 835 MB, over three times the 256 MB Infinity Cache), so
+    each launch streams its weights from HBM; each M is timed as a loop of back-to-back kernel
+    launches with events around the loop.  M = 1 and M = 512 are checked on sampled rows."""
     import torch
-    K, N, sid = 5120, 25600, 2
-    layers = [quant_layer(K, N, "int4", sid, seed=1000 + sid + 17 * i, opts={"group_size": 128})[0] for i in range(4)]
-    out = {}
-    for M in (1, 16, 64, 128, 256, 512):
+    import oracle
+    from powershard_amd import ops
+    K, N, sid, copies = 5120, 25600, 2, 12
+    layers = [quant_layer(K, N, "int4", sid, seed=1000 + sid + 17 * i, opts={"group_size": 128}) for i in range(copies)]
+    ws = [(qt._qdata, qt._params.scale, qt._params.zero, b) for _, qt, b in layers]
+    out, parity = {}, {}
+    for M in (1, 16, 32, 64, 128, 256, 512):
         x = activations(M, K, sid, outlier_scale=1.0)
         it = [0]
 
         def step():
-            with torch.no_grad():
-                layers[it[0] % 4](x)
+            q, sc, z, b = ws[it[0] % copies]
+            ops.gemm_w4a16(x, q, sc, z, 128, b)
             it[0] += 1
-        ms, per = timed_steps(step, max(args.steps, 20), args.warmup)
-        kms = per["gemm_w4a16"]
+        kms = untimed_kernel_ms(step, max(args.steps, 24), max(args.warmup, 12))
         wbytes = N * K // 2 + 2 * 2 * N * (K // 128)
         algo_bytes = wbytes + M * K * 2 + M * N * 2
         flops = 2.0 * M * N * K
@@ -278,29 +432,51 @@ def extra_int4(args):
                       hbm_frac=algo_bytes / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                       tflops=flops / (kms * 1e-3) / 1e12, bf16_mfma_frac=flops / (kms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS)
         log(f"[bench] int4 M={M}: {kms * 1e3:.1f} us, {out[M]['hbm_gbs']:.0f} GB/s, {out[M]['tflops']:.1f} TFLOP/s")
-    del layers
+        if M in (1, 512):
+            layer, qt, b = layers[0]
+            with torch.no_grad():
+                y = layer(x)
+            rows = sample_rows(M, 64, 6000 + M)
+            p = qt._params
+            wd = oracle.dequant_uint4(qt._qdata.cpu(), p.scale.cpu(), p.zero.cpu(), 128)
+            ref = oracle.gemm_wonly(x[rows.to(x.device)].cpu(), wd, None, b.cpu(), out_dtype=torch.float32)
+            parity[M] = within_bar(y[rows.to(y.device)].cpu(), ref)
+            log(f"[bench] int4 M={M} parity: {parity[M]}")
+    del layers, ws
     torch.cuda.empty_cache()
-    return dict(workload="W4A16 uint4 asym g128, K=5120->N=25600", sweep=out)
+    return dict(workload="W4A16 uint4 asym g128, K=5120->N=25600", weight_copies=copies, sweep=out, parity=parity)
 
 
 def extra_fp8(args):
     import torch
+    import oracle
     M, K, N, sid = 32760, 5120, 15360, 3
     x = activations(M, K, sid, outlier_scale=1.0)
-    layer = quant_layer(K, N, "fp8", sid)[0]
+    layer, qt, b = quant_layer(K, N, "fp8", sid)
 
     def step():
         with torch.no_grad():
             layer(x)
-    ms, per = timed_steps(step, args.steps, args.warmup)
+    ms = untimed_kernel_ms(step, args.steps, args.warmup)
+    from powershard_amd import ops
+    qx, sx = ops.quantize_rows(x, fp8=True)
+    gemm_ms = untimed_kernel_ms(lambda: ops.gemm_fp8(qx, sx, qt._qdata, qt._params.scale, b), args.steps, 3)
+    quant_ms = untimed_kernel_ms(lambda: ops.quantize_rows(x, fp8=True), args.steps, 3)
     flops = 2.0 * M * N * K
     res = dict(workload="fp8 e4m3 per-token x per-tensor, Wan-14B QKV 5120->15360, M=32760", ms_per_step=ms,
-               tflops=flops / (ms * 1e-3) / 1e12, gemm_ms=per["gemm_fp8"],
-               gemm_tflops=flops / (per["gemm_fp8"] * 1e-3) / 1e12,
-               gemm_frac=flops / (per["gemm_fp8"] * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
-               quant_ms=per["quantize_rows_fp8"])
-    log(f"[bench] fp8: {ms:.3f} ms/step, gemm {res['gemm_tflops']:.0f} TFLOP/s ({100 * res['gemm_frac']:.1f}%)")
-    del layer, x
+               tflops=flops / (ms * 1e-3) / 1e12, gemm_ms=gemm_ms, gemm_tflops=flops / (gemm_ms * 1e-3) / 1e12,
+               gemm_frac=flops / (gemm_ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, quant_ms=quant_ms)
+    with torch.no_grad():
+        y = layer(x)
+    rows = sample_rows(M, 64, 6003)
+    xr = x[rows.to(x.device)].cpu()
+    qa, sa = oracle.quantize_rows_fp8(xr)
+    ref = oracle.gemm_fp8(qa, sa, qt._qdata.cpu().view(torch.uint8), qt._params.scale.cpu(), b.cpu(),
+                          out_dtype=torch.float32)
+    res["parity"] = within_bar(y[rows.to(y.device)].cpu(), ref)
+    log(f"[bench] fp8: {ms:.3f} ms/step, gemm {res['gemm_tflops']:.0f} TFLOP/s ({100 * res['gemm_frac']:.1f}%); "
+        f"parity {res['parity']}")
+    del layer, x, qx, sx, y
     torch.cuda.empty_cache()
     return res
 
@@ -340,8 +516,20 @@ def extra_wan_stack(args):
                ms_total=ms, ms_per_block=ms / 40, tops=40 * ops_per_block / (ms * 1e-3) / 1e12,
                frac_int8_peak=40 * ops_per_block / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
                quant_ms_mean=per["quantize_rows_i8"], gemm_ms_mean=per["gemm_i8"])
-    log(f"[bench] wan stack: {ms:.1f} ms total, {ms / 40:.2f} ms/block, {res['tops']:.0f} TOPS")
-    del blocks, x, h
+    # parity: block 0's FFN up projection on the heavy-tailed input, 64 sampled rows, bit-exact
+    import oracle
+    from powershard_amd import quant_linear as ql
+    up = blocks[0][4]
+    with torch.no_grad():
+        y = up(x)
+    qt0 = ql.unpack(up.qbytes, up._ps_qplan)
+    rows = sample_rows(M, 64, 6004)
+    qa, sa = oracle.quantize_rows_i8(x[rows.to(x.device)].cpu(), 256)
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, qt0._qdata.cpu()), sa, qt0._params.scale.cpu(), up.bias.cpu())
+    res["parity"] = dict(rows_checked=64, layer="block 0 ffn up",
+                         bitexact=bool(torch.equal(y[rows.to(y.device)].cpu().view(torch.int16), ref.view(torch.int16))))
+    log(f"[bench] wan stack: {ms:.1f} ms total, {ms / 40:.2f} ms/block, {res['tops']:.0f} TOPS; parity {res['parity']}")
+    del blocks, x, h, y
     torch.cuda.empty_cache()
     return res
 
@@ -460,11 +648,16 @@ def extra_w8a16(args):
 
     def step():
         ops.gemm_w8a16(x, q, s, b)
-    ms, per = timed_steps(step, max(args.steps, 20), args.warmup)
+    kms = untimed_kernel_ms(step, max(args.steps, 20), args.warmup)
     flops = 2.0 * M * N * K
-    res = dict(workload="int8 weight-only (W8A16) 1024x5120x5120", kernel_ms=per["gemm_w8a16"],
-               tflops=flops / (per["gemm_w8a16"] * 1e-3) / 1e12)
-    log(f"[bench] w8a16: {per['gemm_w8a16'] * 1e3:.1f} us, {res['tflops']:.0f} TFLOP/s")
+    res = dict(workload="int8 weight-only (W8A16) 1024x5120x5120", kernel_ms=kms, tflops=flops / (kms * 1e-3) / 1e12)
+    import oracle
+    y = ops.gemm_w8a16(x, q, s, b)
+    rows = sample_rows(M, 64, 6000)
+    ref = oracle.gemm_wonly(x[rows.to(x.device)].cpu(), q.cpu().to(torch.bfloat16), s.cpu(), b.cpu(),
+                            out_dtype=torch.float32)
+    res["parity"] = within_bar(y[rows.to(y.device)].cpu(), ref)
+    log(f"[bench] w8a16: {kms * 1e3:.1f} us, {res['tflops']:.0f} TFLOP/s; parity {res['parity']}")
     # Int8Linear (powershard/operations.py:96-132) with ConvRot storage on the same shape: the kernel
     # path (rotate + W8A16) against the reference's 256-row tile dequantization + F.linear
     from powershard_amd.operations import Int8Linear
@@ -509,9 +702,11 @@ def main():
     h, sample = headline(args)
     parity = check_headline_parity(sample)
     log(f"[bench] headline parity ({parity['rows_checked']} sampled rows vs oracle): {parity}")
-    cpu = None if args.no_cpu else cpu_baseline(sample, args.cpu_seconds)
-    if cpu:
-        log(f"[bench] cpu baseline: {cpu['value'] * 1e3:.1f} GOPS on {cpu['cores']} threads")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(sample, cpu_inputs(sample), args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value'] * 1e3:.1f} GOPS on {cpu['cores']} threads "
+            f"({cpu['single_thread']['value'] * 1e3:.1f} on one), {cpu['cpu_model']}")
     extra = {}
     if not args.no_extra:
         for name, fn in (("int4_w4a16", extra_int4), ("fp8", extra_fp8), ("w8a16", extra_w8a16),
@@ -528,6 +723,7 @@ def main():
     roof = dict(bound="mfma", achieved=h["gemm_tops"], peak=PEAK_INT8_TOPS, unit="TOPS",
                 frac=h["gemm_tops"] / PEAK_INT8_TOPS, traffic=traffic and traffic["bytes"], kernel="gemm_i8",
                 kernel_ms=h["gemm_ms"], algorithmic_ops_per_launch=2.0 * h["M"] * h["N"] * h["K"],
+                timing="HIP events on the launch stream around back-to-back launches of the GEMM alone",
                 traffic_source=traffic and traffic["source"])
     line = {
         "metric": METRIC, "value": round(h["tops"], 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
