@@ -17,6 +17,7 @@ LIB_PATH = Path(os.environ.get("PSQUANT_LIB", Path(__file__).resolve().parent / 
 ABI_VERSION = 1
 
 BF16, F16, F32 = 0, 1, 2
+W_UINT4, W_INT8 = 0, 1   # enum psq_weight_kind
 
 # Every exported entry point: name -> (restype, argtypes).  Mirrors include/psquant.h.
 _P, _I64, _I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
@@ -34,6 +35,9 @@ SIGNATURES = {
     "psq_gemm_fp8_act": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_w4a16": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_w8a16": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
+    "psq_gemm_wonly_workspace_bytes": (_I64, [_I, _I64, _I64, _I64, _I64, _I]),
+    "psq_gemm_w4a16_ws": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "psq_gemm_w8a16_ws": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "psq_dequant_uint4": (_I, [_P, _P, _P, _I, _I64, _I64, _P, _I, _P]),
     "psq_dequant_i8_rows": (_I, [_P, _P, _I64, _I64, _I, _P, _I, _P]),
     "psq_dequant_fp8": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _P]),

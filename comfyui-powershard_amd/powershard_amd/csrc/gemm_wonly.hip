@@ -35,6 +35,11 @@ struct WArgs {
     void *y;
     int y_dtype;
     int64_t ldy;
+    // split-K of the tiled kernel (ksplit > 1): per output tile, ksplit workgroups take
+    // contiguous ranges of its K stages and write their fp32 partial tiles to `part`; a second
+    // kernel adds them in split order and applies the epilogue
+    int ksplit = 1;
+    float *part = nullptr;      // [tile row][tile column][ksplit][BM][256] fp32
 };
 
 template <int XDT>
@@ -248,10 +253,15 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int frow = lane & 31, h = lane >> 5;
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
+    const int S = wa.ksplit;                                 // workgroups per tile (split-K)
+    const int tile = (int)(blockIdx.x / (unsigned)S), split = (int)blockIdx.x - tile * S;
     int pm, pn;
-    tile_order(blockIdx.x, nbm, nbn, 4, pm, pn);
+    tile_order(tile, nbm, nbn, 4, pm, pn);
     const int m0 = pm * BM, n0 = pn * BN;
-    const int nk = K / BK;
+    // this workgroup's K stages [kb, kb + nk) of the tile (all of them without a split)
+    const int nk_all = K / BK;
+    const int kb = (int)((int64_t)split * nk_all / S);
+    const int nk = (int)((int64_t)(split + 1) * nk_all / S) - kb;
     const int G = WK == W_UINT4 ? K / wa.gs : 1;
     const int64_t wld = WK == W_UINT4 ? K / 2 : K;          // weight row bytes
 
@@ -359,7 +369,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
 
     // ---- prologue: stages 0 .. NSTAGE-2 in flight, stage 0 landed, its first fragments ready
 #pragma unroll
-    for (int st = 0; st < NSTAGE - 1; st++) issue_all(st, min(st, nk - 1));
+    for (int st = 0; st < NSTAGE - 1; st++) issue_all(st, kb + min(st, nk - 1));
     wait_vmcnt<(NSTAGE - 2) * LPS>();
     stage_barrier();
     WRaw wr;
@@ -407,7 +417,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
 #pragma clang loop unroll(disable)
     for (int kt = 0; kt < nk; kt++) {
         const int fill = rs == 0 ? NSTAGE - 1 : rs - 1;     // ring slot of stage kt + NSTAGE - 1
-        const int kfill = min(kt + NSTAGE - 1, nk - 1);      // (past the end: re-load the last stage)
+        const int kfill = kb + min(kt + NSTAGE - 1, nk - 1); // (past the end: re-load the last stage)
         const int nxt = rs == NSTAGE - 1 ? 0 : rs + 1;
         using I = std::integral_constant<int, 0>;
         kstep(std::integral_constant<int, 1>{}, I{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
@@ -421,6 +431,27 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         rs = nxt;
     }
     wait_vmcnt<0>();   // the re-issued tail loads land before the workgroup's LDS is released
+
+    // ---- split-K (128-row tiles only): this K range's partial tile, row-major, for the reduction
+    if constexpr (BM == 128) if (S > 1) {
+        float *part = wa.part + (((int64_t)pm * nbn + pn) * S + split) * (BM * BN);
+        static_for<TM>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            static_for<TN>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                static_for<4>([&](auto gc) {
+                    constexpr int g = decltype(gc)::value;
+                    // lane (row 32 i + frow) holds columns 64 wave + 32 j + 8 g + 4 h + 0..3
+                    float *o = part + (32 * i + frow) * BN + 64 * wave + 32 * j + 8 * g + 4 * h;
+                    *(v4f *)o = v4f{__int_as_float(agpr_read(acc[i][j][4 * g])),
+                                    __int_as_float(agpr_read(acc[i][j][4 * g + 1])),
+                                    __int_as_float(agpr_read(acc[i][j][4 * g + 2])),
+                                    __int_as_float(agpr_read(acc[i][j][4 * g + 3]))};
+                });
+            });
+        });
+        return;
+    }
 
     // ---- epilogue: acc[i][j] is the transposed 32 x 32 tile, lane (l & 31) holds output row
     // m = m0 + 32 i + (l & 31), register 4g + c column n = n0 + 64 wave + 32 j + 8 g + 4 h + c.
@@ -759,9 +790,36 @@ void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t
     else gemm_wonly_skinny<XDT, WK, 4><<<grid, block, 0, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
 }
 
-// The skinny kernel takes M <= SKINNY_MAX_M when K is a whole number of 128-element blocks (and,
-// for uint4, the groups hold whole 32-element lane runs); the tiled kernel takes the rest.
-constexpr int64_t SKINNY_MAX_M = 64;
+constexpr int64_t SKINNY_MAX_M = 64;   // largest M of the streaming and skinny kernels
+
+// Split-K reduction: y = round_out(fmaf(((p_0 + p_1) + ...) + p_{S-1}, cs[n], bias[n])) over the
+// partial tiles of the tiled kernel (cs = the int8 row scale, 1 for uint4), the tiled kernel's
+// epilogue on the sum taken in split order.  One thread per 4 consecutive columns of a row.
+template <int BM>
+__global__ void __launch_bounds__(256)
+wonly_splitk_reduce(const float *__restrict__ part, int S, int M, int N, WArgs wa)
+{
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int nq = (N + 3) / 4;
+    if (id >= (int64_t)M * nq) return;
+    const int m = (int)(id / nq), n = (int)(id % nq) * 4;
+    const int nbn = (N + wt::BN - 1) / wt::BN;
+    const int pm = m / BM, pn = n / wt::BN;
+    const float *p = part + ((int64_t)pm * nbn + pn) * S * (BM * wt::BN) + (m - pm * BM) * wt::BN + (n - pn * wt::BN);
+    v4f t = *(const v4f *)p;
+    for (int sp = 1; sp < S; sp++) {
+        const v4f u = *(const v4f *)(p + (int64_t)sp * (BM * wt::BN));
+        t = v4f{t[0] + u[0], t[1] + u[1], t[2] + u[2], t[3] + u[3]};
+    }
+    uint8_t *row = (uint8_t *)wa.y + (int64_t)m * wa.ldy * (wa.y_dtype == PSQ_F32 ? 4 : 2);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        if (n + c >= N) break;
+        const float cs = wa.scale32 ? wa.scale32[n + c] : 1.0f;
+        const float b = wa.bias ? load_elem(wa.bias, n + c, wa.bias_dtype) : 0.0f;
+        store_elem(row, n + c, wa.y_dtype, __builtin_fmaf(t[c], cs, b));
+    }
+}
 
 template <int XDT, int WK, int BM>
 int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
@@ -778,45 +836,121 @@ int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_
         attr_set[dev] = true;
     }
     const int64_t tiles = ((M + BM - 1) / BM) * ((N + wt::BN - 1) / wt::BN);
-    kern<<<dim3((unsigned)tiles), dim3(NTHREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    kern<<<dim3((unsigned)(tiles * wa.ksplit)), dim3(NTHREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    if (wa.ksplit > 1) {
+        if (int e = check_launch(name)) return e;
+        const int64_t threads = M * ((N + 3) / 4);
+        wonly_splitk_reduce<BM><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st>>>(wa.part, wa.ksplit,
+                                                                                             (int)M, (int)N, wa);
+    }
     return check_launch(name);
 }
 
 #ifndef PSQ_WT_FILL
 #define PSQ_WT_FILL 1
 #endif
-// 128-row tiles when they still fit one wave of workgroups on the GPU (twice the tiles of the
-// 256-row ones, each with half the MFMA work and the same dequantization), else 256-row tiles.
-template <int XDT, int WK>
-int launch_tiled(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
-                 const char *name)
+// Split-K cost model: a split of s runs 1/s of a tile's K per workgroup, and each extra split adds
+// its ring prologue and its partial tile's round trip through memory.  Splits stay within one round
+// of workgroups (tiles s <= CUs): at c0 (160 tiles) three splits in two rounds measured slower than
+// none (99 against 89 us), while two splits of M = 128 x N = 25600 (100 tiles) took 89 to 65 us.
+#ifndef PSQ_WT_SPLIT_COST
+#define PSQ_WT_SPLIT_COST 0.05
+#endif
+constexpr int kMaxSplit = 8;
+constexpr int64_t kMaxPartBytes = 64LL << 20;                   // partial tiles of one launch
+
+// The tiled kernel's launch: 128-row tiles when they still fit one wave of workgroups on the GPU
+// (twice the tiles of the 256-row ones, each with half the MFMA work and the same
+// dequantization), else 256-row tiles; and, when the tiles leave CUs idle, the K split with the
+// fewest rounds per unit of work.  Workspace: the partial tiles.
+struct TiledPlan {
+    int bm = 128;
+    int64_t tiles = 0;
+    int ksplit = 1;
+    int64_t ws_bytes = 0;
+};
+
+TiledPlan plan_tiled(int64_t M, int64_t N, int64_t K, int cus)
 {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
-    const int64_t tiles128 = ((M + 127) / 128) * ((N + wt::BN - 1) / wt::BN);
-    if (tiles128 <= PSQ_WT_FILL * cu_count(dev)) return launch_tiled_bm<XDT, WK, 128>(x, ldx, M, N, K, wa, st, name);
-    return launch_tiled_bm<XDT, WK, 256>(x, ldx, M, N, K, wa, st, name);
+    TiledPlan p;
+    const int64_t nbn = (N + wt::BN - 1) / wt::BN;
+    p.bm = ((M + 127) / 128) * nbn <= PSQ_WT_FILL * cus ? 128 : 256;
+    p.tiles = ((M + p.bm - 1) / p.bm) * nbn;
+    const int64_t nk = K / wt::BK;
+    double best = 1.0;
+    if (p.bm == 128 && p.tiles < cus) {   // the kernel splits 128-row tiles
+        for (int s = 2; s <= kMaxSplit && 4 * s <= nk && p.tiles * s <= cus; s++) {
+            const double t = 1.0 / s + PSQ_WT_SPLIT_COST * (s - 1);
+            if (t < best - 1e-9 && p.tiles * s * p.bm * wt::BN * 4 <= kMaxPartBytes) {
+                best = t;
+                p.ksplit = s;
+            }
+        }
+    }
+    p.ws_bytes = p.ksplit > 1 ? p.tiles * p.ksplit * p.bm * wt::BN * 4 : 0;
+    return p;
 }
 
+// The weight-streaming kernel takes the uint4 shapes with M <= SKINNY_MAX_M and groups of a
+// multiple of 128; the skinny kernel takes M <= SKINNY_MAX_M when K is a whole number of
+// 128-element blocks (and, for uint4, the groups hold whole 32-element lane runs); the tiled
+// kernel takes the rest.
+enum class Path { Stream, Skinny, Tiled };
+
+Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
+{
+    if (wk == W_UINT4 && PSQ_W4_STREAM && M <= SKINNY_MAX_M && gs % 128 == 0 &&
+        K % (M <= 16 ? ws::BLK<1>() : ws::BLK<2>()) == 0 && ldx <= (1LL << 22))
+        return Path::Stream;
+    if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (wk != W_UINT4 || gs % 32 == 0)) return Path::Skinny;
+    return Path::Tiled;
+}
+
+// Workspace bytes of a call (0: no split); the split needs a device, else 0.
+int64_t workspace_bytes(int wk, int64_t ldx, int64_t M, int64_t N, int64_t K, int gs)
+{
+    if (M <= 0 || N <= 0 || K <= 0 || choose_path(wk, ldx, M, K, gs) != Path::Tiled) return 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    return plan_tiled(M, N, K, cu_count(dev)).ws_bytes;
+}
+
+// workspace: NULL = no split; else at least workspace_bytes() (no contents carried between calls).
 template <int WK>
-int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa,
-           hipStream_t st, const char *name)
+int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_t K, WArgs wa,
+           void *workspace, int64_t ws_bytes, hipStream_t st, const char *name)
 {
     const uint16_t *xp = (const uint16_t *)x;
-    if (WK == W_UINT4 && PSQ_W4_STREAM && M <= SKINNY_MAX_M && wa.gs % 128 == 0 &&
-        K % (M <= 16 ? ws::BLK<1>() : ws::BLK<2>()) == 0 && ldx <= (1LL << 22)) {
+    const Path path = choose_path(WK, ldx, M, K, wa.gs);
+    if (path == Path::Stream)
         return x_dtype == PSQ_BF16 ? launch_stream<PSQ_BF16>(xp, ldx, M, N, K, wa, st, name)
                                    : launch_stream<PSQ_F16>(xp, ldx, M, N, K, wa, st, name);
-    }
-    if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (WK != W_UINT4 || wa.gs % 32 == 0)) {
+    if (path == Path::Skinny) {
         if (x_dtype == PSQ_BF16) launch_skinny<PSQ_BF16, WK>(xp, ldx, M, N, K, wa, st);
         else launch_skinny<PSQ_F16, WK>(xp, ldx, M, N, K, wa, st);
         return check_launch(name);
     }
     if (ldx > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: ldx above 2^22", name);   // 32-bit row offsets
     if (K > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: K above 2^22", name);       // (of the weights too)
-    return x_dtype == PSQ_BF16 ? launch_tiled<PSQ_BF16, WK>(xp, ldx, M, N, K, wa, st, name)
-                               : launch_tiled<PSQ_F16, WK>(xp, ldx, M, N, K, wa, st, name);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
+    const TiledPlan plan = plan_tiled(M, N, K, cu_count(dev));
+    wa.ksplit = 1;
+    if (workspace && plan.ksplit > 1) {
+        if (ws_bytes < plan.ws_bytes)
+            return set_error(PSQ_E_ARG, "%s: workspace of %lld bytes, %lld needed", name, (long long)ws_bytes,
+                             (long long)plan.ws_bytes);
+        if ((uintptr_t)workspace & 255) return set_error(PSQ_E_ARG, "%s: workspace must be 256-byte aligned", name);
+        wa.ksplit = plan.ksplit;
+        wa.part = (float *)workspace;
+    }
+    const bool bm128 = plan.bm == 128;
+    auto go = [&](auto xc) {
+        constexpr int XDT = decltype(xc)::value;
+        return bm128 ? launch_tiled_bm<XDT, WK, 128>(xp, ldx, M, N, K, wa, st, name)
+                     : launch_tiled_bm<XDT, WK, 256>(xp, ldx, M, N, K, wa, st, name);
+    };
+    return x_dtype == PSQ_BF16 ? go(std::integral_constant<int, PSQ_BF16>{}) : go(std::integral_constant<int, PSQ_F16>{});
 }
 
 int check_common(const char *name, const void *x, int x_dtype, int64_t ldx, const void *wq, const void *y, int y_dtype,
@@ -835,6 +969,34 @@ int check_common(const char *name, const void *x, int x_dtype, int64_t ldx, cons
     return PSQ_OK;
 }
 
+// One weight-only GEMM call (the checks of every entry point, then the launch).
+int gemm_w4a16(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq, const uint16_t *w_scale,
+               const uint16_t *w_zero, int group_size, const void *bias, int bias_dtype, void *y, int y_dtype,
+               int64_t ldy, int64_t M, int64_t N, int64_t K, void *workspace, int64_t ws_bytes, void *stream,
+               const char *name)
+{
+    if (int e = check_common(name, x, x_dtype, ldx, wq, y, y_dtype, ldy, bias, bias_dtype, M, N, K)) return e;
+    if (M == 0 || N == 0) return PSQ_OK;
+    if (!w_scale || !w_zero) return set_error(PSQ_E_ARG, "%s: null scale/zero", name);
+    if (group_size <= 0 || group_size % KSTAGE || K % group_size)
+        return set_error(PSQ_E_SHAPE, "%s: group size %d must be a multiple of %d dividing K", name, group_size, KSTAGE);
+    if (int e = require_device()) return e;
+    WArgs wa{wq, w_scale, w_zero, nullptr, group_size, bias, bias_dtype, y, y_dtype, ldy};
+    return launch<W_UINT4>(x, x_dtype, ldx, M, N, K, wa, workspace, ws_bytes, (hipStream_t)stream, name);
+}
+
+int gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t *wq, const float *w_scale, const void *bias,
+               int bias_dtype, void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *workspace,
+               int64_t ws_bytes, void *stream, const char *name)
+{
+    if (int e = check_common(name, x, x_dtype, ldx, wq, y, y_dtype, ldy, bias, bias_dtype, M, N, K)) return e;
+    if (M == 0 || N == 0) return PSQ_OK;
+    if (!w_scale) return set_error(PSQ_E_ARG, "%s: null scale", name);
+    if (int e = require_device()) return e;
+    WArgs wa{(const uint8_t *)wq, nullptr, nullptr, w_scale, 0, bias, bias_dtype, y, y_dtype, ldy};
+    return launch<W_INT8>(x, x_dtype, ldx, M, N, K, wa, workspace, ws_bytes, (hipStream_t)stream, name);
+}
+
 }  // namespace
 }  // namespace psq
 
@@ -844,27 +1006,38 @@ int psq_gemm_w4a16(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq, c
                    const uint16_t *w_zero, int group_size, const void *bias, int bias_dtype, void *y, int y_dtype,
                    int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
 {
-    using namespace psq;
-    if (int e = check_common("gemm_w4a16", x, x_dtype, ldx, wq, y, y_dtype, ldy, bias, bias_dtype, M, N, K)) return e;
-    if (M == 0 || N == 0) return PSQ_OK;
-    if (!w_scale || !w_zero) return set_error(PSQ_E_ARG, "gemm_w4a16: null scale/zero");
-    if (group_size <= 0 || group_size % KSTAGE || K % group_size)
-        return set_error(PSQ_E_SHAPE, "gemm_w4a16: group size %d must be a multiple of %d dividing K", group_size, KSTAGE);
-    if (int e = require_device()) return e;
-    WArgs wa{wq, w_scale, w_zero, nullptr, group_size, bias, bias_dtype, y, y_dtype, ldy};
-    return launch<W_UINT4>(x, x_dtype, ldx, M, N, K, wa, (hipStream_t)stream, "gemm_w4a16");
+    return psq::gemm_w4a16(x, x_dtype, ldx, wq, w_scale, w_zero, group_size, bias, bias_dtype, y, y_dtype, ldy, M, N,
+                           K, nullptr, 0, stream, "gemm_w4a16");
+}
+
+int psq_gemm_w4a16_ws(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq, const uint16_t *w_scale,
+                      const uint16_t *w_zero, int group_size, const void *bias, int bias_dtype, void *y, int y_dtype,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, void *workspace, int64_t workspace_bytes,
+                      void *stream)
+{
+    return psq::gemm_w4a16(x, x_dtype, ldx, wq, w_scale, w_zero, group_size, bias, bias_dtype, y, y_dtype, ldy, M, N,
+                           K, workspace, workspace_bytes, stream, "gemm_w4a16");
 }
 
 int psq_gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t *wq, const float *w_scale, const void *bias,
                    int bias_dtype, void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
 {
-    using namespace psq;
-    if (int e = check_common("gemm_w8a16", x, x_dtype, ldx, wq, y, y_dtype, ldy, bias, bias_dtype, M, N, K)) return e;
-    if (M == 0 || N == 0) return PSQ_OK;
-    if (!w_scale) return set_error(PSQ_E_ARG, "gemm_w8a16: null scale");
-    if (int e = require_device()) return e;
-    WArgs wa{(const uint8_t *)wq, nullptr, nullptr, w_scale, 0, bias, bias_dtype, y, y_dtype, ldy};
-    return launch<W_INT8>(x, x_dtype, ldx, M, N, K, wa, (hipStream_t)stream, "gemm_w8a16");
+    return psq::gemm_w8a16(x, x_dtype, ldx, wq, w_scale, bias, bias_dtype, y, y_dtype, ldy, M, N, K, nullptr, 0,
+                           stream, "gemm_w8a16");
+}
+
+int psq_gemm_w8a16_ws(const void *x, int x_dtype, int64_t ldx, const int8_t *wq, const float *w_scale,
+                      const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
+                      int64_t K, void *workspace, int64_t workspace_bytes, void *stream)
+{
+    return psq::gemm_w8a16(x, x_dtype, ldx, wq, w_scale, bias, bias_dtype, y, y_dtype, ldy, M, N, K, workspace,
+                           workspace_bytes, stream, "gemm_w8a16");
+}
+
+int64_t psq_gemm_wonly_workspace_bytes(int weight_kind, int64_t ldx, int64_t M, int64_t N, int64_t K, int group_size)
+{
+    if (weight_kind != PSQ_W_UINT4 && weight_kind != PSQ_W_INT8) return 0;
+    return psq::workspace_bytes(weight_kind == PSQ_W_UINT4 ? psq::W_UINT4 : psq::W_INT8, ldx, M, N, K, group_size);
 }
 
 }  // extern "C"

@@ -224,10 +224,27 @@ def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activa
     return y
 
 
+# Split-K workspaces of the weight-only GEMMs, one per (device, stream): calls on one stream run in
+# order, so they can share it; replaced by a larger one when a call needs more.
+_workspaces = {}
+
+
+def _workspace(device, stream, nbytes):
+    if nbytes <= 0:
+        return None, 0
+    key = (device.index, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws, ws.numel()
+
+
 def gemm_w4a16(x, wq, w_scale, w_zero, group_size, bias=None, out_dtype=None):
     """uint4 asymmetric group weights, in-register dequantized onto bf16/f16 MFMA.
 
     x [M, K] bf16/f16, wq [N, K/2] uint8 (low nibble = even k), w_scale/w_zero [N, K/group] fp16.
+    Shapes that leave CUs idle split K across workgroups through a cached workspace.
     """
     _need_gpu(x, wq, w_scale, w_zero)
     x, wq = _rows2d(x), wq.contiguous()
@@ -239,9 +256,12 @@ def gemm_w4a16(x, wq, w_scale, w_zero, group_size, bias=None, out_dtype=None):
     w_zero = w_zero.to(torch.float16).contiguous()
     bias, bdt = _bias(bias, N, x.device)
     y = torch.empty(M, N, dtype=out_dtype or x.dtype, device=x.device)
-    _launch("gemm_w4a16", _native.lib().psq_gemm_w4a16, _p(x), _dt(x, "x"), x.stride(0), _p(wq), _p(w_scale), _p(w_zero),
-                                               int(group_size), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K,
-                                               _stream(x))
+    stream = _stream(x)
+    ws, nb = _workspace(x.device, stream.value,
+                        _native.lib().psq_gemm_wonly_workspace_bytes(_native.W_UINT4, x.stride(0), M, N, K,
+                                                                     int(group_size)))
+    _launch("gemm_w4a16", _native.lib().psq_gemm_w4a16_ws, _p(x), _dt(x, "x"), x.stride(0), _p(wq), _p(w_scale),
+            _p(w_zero), int(group_size), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K, _p(ws), nb, stream)
     return y
 
 
@@ -254,8 +274,11 @@ def gemm_w8a16(x, wq, w_scale, bias=None, out_dtype=None):
     w_scale = w_scale.to(torch.float32).reshape(-1).contiguous()
     bias, bdt = _bias(bias, N, x.device)
     y = torch.empty(M, N, dtype=out_dtype or x.dtype, device=x.device)
-    _launch("gemm_w8a16", _native.lib().psq_gemm_w8a16, _p(x), _dt(x, "x"), x.stride(0), _p(wq), _p(w_scale), _p(bias), bdt,
-                                               _p(y), _dt(y, "out"), N, M, N, K, _stream(x))
+    stream = _stream(x)
+    ws, nb = _workspace(x.device, stream.value,
+                        _native.lib().psq_gemm_wonly_workspace_bytes(_native.W_INT8, x.stride(0), M, N, K, 0))
+    _launch("gemm_w8a16", _native.lib().psq_gemm_w8a16_ws, _p(x), _dt(x, "x"), x.stride(0), _p(wq), _p(w_scale),
+            _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K, _p(ws), nb, stream)
     return y
 
 

@@ -168,6 +168,33 @@ PSQ_API int psq_gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t
                    const float *w_scale, const void *bias, int bias_dtype, void *y,
                    int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream);
 
+/* Split-K workspace of the weight-only GEMMs.  When M, N and K leave CUs idle under the tiled
+ * kernel (M > 64, e.g. M = 128 at N = 25600: 100 output tiles of 128 x 256 for 256 CUs), the *_ws
+ * entry points split each tile's K range over up to 8 workgroups, which write fp32 partial tiles
+ * to the workspace; a second kernel on the same stream adds them in split order (a fixed order:
+ * results do not depend on timing) and applies the epilogue.  Same outputs and bars as
+ * psq_gemm_w4a16 / psq_gemm_w8a16 (a different fp32 summation order).  No counterpart in the
+ * reference (the caller-allocated workspace follows the ownership rule above); the callers are
+ * the int4 and int8 weight-only linears of the text encoder and Int8Linear.
+ *   workspace        NULL: no split (exactly psq_gemm_w4a16 / psq_gemm_w8a16); else 256-byte
+ *                    aligned and at least psq_gemm_wonly_workspace_bytes() bytes.  Nothing in it
+ *                    is carried between calls, but calls that share it must not overlap (use
+ *                    one workspace per stream). */
+enum psq_weight_kind { PSQ_W_UINT4 = 0, PSQ_W_INT8 = 1 };
+
+/* Bytes of workspace a *_ws call of this shape uses on the current device (0: no split). */
+PSQ_API int64_t psq_gemm_wonly_workspace_bytes(int weight_kind, int64_t ldx, int64_t M, int64_t N, int64_t K,
+                                               int group_size);
+PSQ_API int psq_gemm_w4a16_ws(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq,
+                      const uint16_t *w_scale, const uint16_t *w_zero, int group_size,
+                      const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,
+                      int64_t M, int64_t N, int64_t K, void *workspace, int64_t workspace_bytes,
+                      void *stream);
+PSQ_API int psq_gemm_w8a16_ws(const void *x, int x_dtype, int64_t ldx, const int8_t *wq,
+                      const float *w_scale, const void *bias, int bias_dtype, void *y,
+                      int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *workspace,
+                      int64_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------- dequantize
  * GPU implementations of QuantizedTensor.dequantize() for the dequantize compute mode
  * (powershard/quant_linear.py:216-220) and of dequantize_rows (operations.py:84-93). */

@@ -279,3 +279,70 @@ def test_int8linear_coherent_activations_stay_finite(gpu):
         ref = tiles(x.to(gpu))
     assert torch.isfinite(y).all()
     assert_bitexact(y, ref, "Int8Linear recomputed on the tiles")
+
+
+# ------------------------------------------------------------ split-K of the tiled kernel
+def _split_plan(M, N, K, gs, kind=0):
+    """Workspace bytes the library asks for (0: no split)."""
+    from powershard_amd import _native
+    return _native.lib().psq_gemm_wonly_workspace_bytes(kind, K, M, N, K, gs)
+
+
+@pytest.mark.parametrize("M,N,K,xdt", [(128, 25600, 5120, torch.bfloat16), (100, 2048, 2048, torch.bfloat16),
+                                       (77, 1280, 1024, torch.float16), (200, 520, 4096, torch.bfloat16)])
+def test_gemm_w4a16_split_k(gpu, M, N, K, xdt):
+    """Shapes whose 128-row tiles leave CUs idle split K over up to 8 workgroups per tile; the last
+    to arrive adds the fp32 partials in split order.  Same bar as the unsplit kernel, and repeated
+    calls are bit-identical (the order does not depend on which workgroup arrives last)."""
+    from powershard_amd import ops
+    gs = 128
+    assert _split_plan(M, N, K, gs) > 0, "shape expected to split"
+    x = heavy_rows(M, K, seed=90 + M, outlier_frac=0, dtype=xdt)
+    w = torch.randn(N, K, generator=seeded(91)) * 0.02
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    b = (torch.randn(N, generator=seeded(92)) * 0.01).to(xdt)
+    args = (x.to(gpu), wq.to(gpu), s.to(gpu), z.to(gpu), gs, b.to(gpu))
+    y32 = ops.gemm_w4a16(*args, out_dtype=torch.float32)
+    again = [ops.gemm_w4a16(*args, out_dtype=torch.float32) for _ in range(3)]
+    for a in again:
+        assert torch.equal(a.view(torch.int32), y32.view(torch.int32)), "split-K result changed between calls"
+    yb = ops.gemm_w4a16(*args, out_dtype=torch.bfloat16)
+    rows = _sample_rows(M, 64, 93) if M > 64 else torch.arange(M)
+    wd = oracle.dequant_uint4(wq, s, z, gs, out_dtype=xdt)
+    assert_fp32_path(y32.cpu()[rows], yb.cpu()[rows], _wonly_rows(x, wd, b, rows), f"w4a16 split-K {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 1024, 2048), (1024, 5120, 5120)])
+def test_gemm_w8a16_split_k(gpu, M, N, K):
+    from powershard_amd import ops
+    x = heavy_rows(M, K, seed=94, outlier_frac=0)
+    w = torch.randn(N, K, generator=seeded(95)) * 0.02
+    q, s = oracle.quantize_weight_int8(w, False)
+    b = (torch.randn(N, generator=seeded(96)) * 0.01).to(torch.bfloat16)
+    args = (x.to(gpu), q.to(gpu), s.to(gpu), b.to(gpu))
+    y32 = ops.gemm_w8a16(*args, out_dtype=torch.float32)
+    yb = ops.gemm_w8a16(*args, out_dtype=torch.bfloat16)
+    rows = _sample_rows(M, 64, 97)
+    ref = oracle.gemm_wonly(x, q.to(torch.bfloat16), s, b, out_dtype=torch.float32, row_ids=rows)
+    assert_fp32_path(y32.cpu()[rows], yb.cpu()[rows], ref, f"w8a16 split-K {M}x{N}x{K}")
+
+
+def test_gemm_w4a16_unsplit_entry_point(gpu):
+    """psq_gemm_w4a16 (no workspace) keeps the unsplit kernel; its output meets the same bar."""
+    import ctypes
+    from powershard_amd import _native
+    M, N, K, gs = 128, 2048, 2048, 128
+    x = heavy_rows(M, K, seed=98, outlier_frac=0).to(gpu)
+    w = torch.randn(N, K, generator=seeded(99)) * 0.02
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    wq, s, z = wq.to(gpu), s.to(gpu), z.to(gpu)
+    y = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    st = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = _native.lib().psq_gemm_w4a16(P(x), _native.BF16, K, P(wq), P(s), P(z), gs, None, 0, P(y), _native.F32,
+                                      N, M, N, K, st)
+    assert rc == 0, _native.last_error()
+    ref = oracle.gemm_wonly(x.cpu(), oracle.dequant_uint4(wq.cpu(), s.cpu(), z.cpu(), gs), None, None,
+                            out_dtype=torch.float32)
+    rms = ref.pow(2).mean().sqrt().item()
+    assert (y.cpu() - ref).abs().max().item() <= 1e-2 * rms
