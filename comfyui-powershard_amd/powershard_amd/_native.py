@@ -38,6 +38,7 @@ SIGNATURES = {
     "psq_gemm_wonly_workspace_bytes": (_I64, [_I, _I64, _I64, _I64, _I64, _I]),
     "psq_gemm_w4a16_ws": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "psq_gemm_w8a16_ws": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "psq_gemm_w4a16_noalloc": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_dequant_uint4": (_I, [_P, _P, _P, _I, _I64, _I64, _P, _I, _P]),
     "psq_dequant_i8_rows": (_I, [_P, _P, _I64, _I64, _I, _P, _I, _P]),
     "psq_dequant_fp8": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _P]),

@@ -12,6 +12,8 @@
 // 256 x 256-tile one for larger M (MFMA-bound), both described where they are defined.
 #include "psq_common.hpp"
 
+#include <mutex>
+
 namespace psq {
 namespace {
 
@@ -997,6 +999,38 @@ int gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t *wq, const 
     return launch<W_INT8>(x, x_dtype, ldx, M, N, K, wa, workspace, ws_bytes, (hipStream_t)stream, name);
 }
 
+// ------------------------------------------------------------------ allocation-free variant
+// psq_gemm_w4a16_noalloc keeps its split-K partial tiles in `scratch`, a file-scope device array of
+// the largest workspace any split plan asks for (kMaxPartBytes = 64 MB), held by every GPU the
+// library runs on until the process ends.  In host code `scratch` names a host-side stand-in, not
+// a device address: its address on a device comes from hipGetSymbolAddress, taken once per device
+// with that device current, and only that address is passed to the kernels.  Nothing in it is
+// carried between calls (a call writes every partial it reads), so nothing needs clearing; calls
+// that overlap on one GPU share it and race.
+static __device__ __align__(256) uint8_t scratch[kMaxPartBytes];
+
+constexpr int kMaxDev = 64;
+std::once_flag g_scratch_once[kMaxDev];
+void *g_scratch_ptr[kMaxDev];
+hipError_t g_scratch_status[kMaxDev];
+
+int scratch_on_device(void **ptr)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev)
+        return set_error(PSQ_E_DEVICE, "gemm_w4a16_noalloc: no current HIP device");
+    std::call_once(g_scratch_once[dev], [dev] {
+        void *p = nullptr;
+        g_scratch_status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = p;
+    });
+    if (g_scratch_status[dev] != hipSuccess || !g_scratch_ptr[dev])
+        return set_error(PSQ_E_DEVICE, "gemm_w4a16_noalloc: no scratch address on device %d: %s", dev,
+                         hipGetErrorString(g_scratch_status[dev]));
+    *ptr = g_scratch_ptr[dev];
+    return PSQ_OK;
+}
+
 }  // namespace
 }  // namespace psq
 
@@ -1032,6 +1066,24 @@ int psq_gemm_w8a16_ws(const void *x, int x_dtype, int64_t ldx, const int8_t *wq,
 {
     return psq::gemm_w8a16(x, x_dtype, ldx, wq, w_scale, bias, bias_dtype, y, y_dtype, ldy, M, N, K, workspace,
                            workspace_bytes, stream, "gemm_w8a16");
+}
+
+int psq_gemm_w4a16_noalloc(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq, const uint16_t *w_scale,
+                           const uint16_t *w_zero, int group_size, const void *bias, int bias_dtype, void *y,
+                           int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
+{
+    using namespace psq;
+    if (M > 0 && N > 0 && K > 0) {
+        if (int e = require_device()) return e;
+        const int64_t need = workspace_bytes(W_UINT4, ldx, M, N, K, group_size);
+        if (need > kMaxPartBytes)
+            return set_error(PSQ_E_SHAPE, "gemm_w4a16_noalloc: %lld bytes of split-K scratch needed, %lld available",
+                             (long long)need, (long long)kMaxPartBytes);
+    }
+    void *ptr = nullptr;
+    if (int e = scratch_on_device(&ptr)) return e;
+    return gemm_w4a16(x, x_dtype, ldx, wq, w_scale, w_zero, group_size, bias, bias_dtype, y, y_dtype, ldy, M, N, K,
+                      ptr, kMaxPartBytes, stream, "gemm_w4a16_noalloc");
 }
 
 int64_t psq_gemm_wonly_workspace_bytes(int weight_kind, int64_t ldx, int64_t M, int64_t N, int64_t K, int group_size)

@@ -195,6 +195,19 @@ PSQ_API int psq_gemm_w8a16_ws(const void *x, int x_dtype, int64_t ldx, const int
                       int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *workspace,
                       int64_t workspace_bytes, void *stream);
 
+/* psq_gemm_w4a16_ws without the workspace argument: the split-K partial tiles live in a static
+ * device array of the library (64 MB on each GPU it runs on, held until the process ends), so the
+ * call allocates nothing -- no hipMalloc, no hipFree, no allocating library routine.  No
+ * counterpart in the reference; it is for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation.  Same arguments and
+ * results as psq_gemm_w4a16_ws with a large enough workspace.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU race.  A shape whose split plan needs more than the
+ * array is refused with PSQ_E_SHAPE (no plan asks for more than 64 MB). */
+PSQ_API int psq_gemm_w4a16_noalloc(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq,
+                           const uint16_t *w_scale, const uint16_t *w_zero, int group_size,
+                           const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,
+                           int64_t M, int64_t N, int64_t K, void *stream);
+
 /* ---------------------------------------------------------------- dequantize
  * GPU implementations of QuantizedTensor.dequantize() for the dequantize compute mode
  * (powershard/quant_linear.py:216-220) and of dequantize_rows (operations.py:84-93). */
