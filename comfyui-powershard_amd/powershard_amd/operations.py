@@ -125,19 +125,17 @@ class Int8Linear(nn.Module):
 
 def install_int8(model, quant, rows):
     """Replace the Linears named in `quant` ({name: {convrot, group_size}}) by Int8Linear; quantized
-    embeddings are left in place and returned."""
-    skipped = {}
-    for name, conf in quant.items():
-        parent_name, _, leaf = name.rpartition(".")
-        parent = model.get_submodule(parent_name)
-        old = getattr(parent, leaf)
-        if isinstance(old, nn.Embedding):
-            skipped[name] = conf
-            continue
-        if not isinstance(old, nn.Linear) or not hasattr(old, "in_features"):
-            raise ValueError(f"INT8 expects a Linear/Embedding (got {type(old).__name__}): {name}")
-        setattr(parent, leaf, Int8Linear(old, conf, rows))
-    return skipped
+    embeddings are left in place and returned ({name: conf}).  Every name is resolved and checked
+    before any module is replaced, so a bad entry leaves the model untouched (ValueError)."""
+    found = {name: model.get_submodule(name) for name in quant}
+    for name, module in found.items():
+        if not isinstance(module, (nn.Linear, nn.Embedding)):
+            raise ValueError(f"INT8 expects a Linear/Embedding (got {type(module).__name__}): {name}")
+    for name, module in found.items():
+        if isinstance(module, nn.Linear):
+            owner, _, leaf = name.rpartition(".")
+            setattr(model.get_submodule(owner) if owner else model, leaf, Int8Linear(module, quant[name], rows))
+    return {name: quant[name] for name, module in found.items() if isinstance(module, nn.Embedding)}
 
 
 @contextmanager

@@ -1,20 +1,21 @@
 """QuantLinear: quantized Linear layers stored as one aligned byte vector, computed by the gfx950
 kernels of libpsquant (native) or by dequantize + F.linear.
 
-Drop-in for powershard/quant_linear.py (ComfyUI-PowerShard 0.6.0):
+Drop-in for powershard/quant_linear.py (ComfyUI-PowerShard 0.6.0).  What a caller or a state dict
+binds to is kept:
 
-* the module / state-dict contract -- ``QuantLinear(src, plan, compute_dtype, native,
+* the module and its state dict -- ``QuantLinear(src, plan, compute_dtype, native,
   follow_input, full_precision)`` with a 1-D ``uint8`` parameter ``qbytes`` and ``bias``
   (quant_linear.py:163-189);
-* the byte layout discipline of ``QuantPlan`` -- components 16-byte aligned, ``_qdata`` first,
-  then the tensor fields of the params dataclass in order, then ``x:<extra>`` (quant_linear.py:27,
-  38-49, 65-122), so FSDP can shard and gather ``qbytes`` as plain bytes;
+* the byte layout of ``QuantPlan`` -- components 16-byte aligned, ``_qdata`` first, then the
+  tensor fields of the params dataclass in order, then ``x:<extra>`` (quant_linear.py:27, 38-49,
+  65-122), so FSDP can shard and gather ``qbytes`` as plain bytes;
 * the compute modes ``native`` / ``dequantize`` / ``auto`` and the fallback convention: a
   native failure of type NotImplementedError / RuntimeError / TypeError / ValueError warns and
   switches the module to dequantize for good; out-of-memory propagates (quant_linear.py:207-215);
 * ``install_quant_linears`` / ``build_bytes`` / ``float_weight`` (quant_linear.py:285-444).
 
-What differs is below the module: ComfyUI's QuantizedTensor is replaced by
+Below the module, ComfyUI's QuantizedTensor is replaced by
 :class:`~powershard_amd.quant_tensor.QuantizedWeight`, and comfy-kitchen's int8_linear /
 torch._scaled_mm / w4a8 ops by the HIP kernels (``native_linear``):
 
@@ -25,15 +26,17 @@ torch._scaled_mm / w4a8 ops by the HIP kernels (``native_linear``):
 """
 import contextlib
 import dataclasses
+import itertools
 import json
-import math
 import threading
 import warnings
+from typing import NamedTuple
 
 import torch
 from torch import nn
 from torch.nn import functional as F
 
+from . import quant_formats as qf
 from . import quant_tensor as qtm
 
 ALIGN = 16
@@ -42,6 +45,27 @@ ALIGN = 16
 EXTRAS = ("pre_quant_scale", "input_scale")
 # Formats with a native kernel here and the library op that runs them.
 NATIVE = {"int8_tensorwise": "gemm_i8", "float8_e4m3fn": "gemm_fp8", "int4_asym_group": "gemm_w4a16"}
+# The exceptions of a native attempt that switch a module to dequantize (quant_linear.py:207-215).
+NATIVE_FAILURES = (NotImplementedError, RuntimeError, TypeError, ValueError)
+
+
+# ------------------------------------------------------------------- the byte plan
+class _Slot(NamedTuple):
+    """One component's place in the byte vector (a plain tuple to the plan's readers)."""
+    name: str
+    dtype: torch.dtype
+    shape: tuple
+    offset: int
+    nbytes: int
+
+
+def _padded(nbytes):
+    return -(-nbytes // ALIGN) * ALIGN
+
+
+def _byte_view(tensor):
+    """The tensor's bytes as a 1-D uint8 view (a contiguous copy first when it is strided)."""
+    return tensor.detach().contiguous().view(-1).view(torch.uint8)
 
 
 @dataclasses.dataclass
@@ -49,7 +73,7 @@ class QuantPlan:
     fmt: str
     layout: object
     params_cls: type
-    fields: dict
+    fields: dict         # the params' non-tensor fields (ConvRot, group size, ...)
     specs: list          # [(name, dtype, shape, offset, nbytes)], "_qdata" first
     total: int
     source: dict         # kind=file|quantize, module, key, table, conf
@@ -57,8 +81,53 @@ class QuantPlan:
     def signature(self):
         return [(n, str(d), list(s), o, b) for n, d, s, o, b in self.specs]
 
+    @classmethod
+    def of(cls, qt, fmt, source, extras=None):
+        tensors, fields = components(qt, extras)
+        sizes = [t.numel() * t.element_size() for _, t in tensors]
+        offsets = itertools.accumulate((_padded(n) for n in sizes), initial=0)
+        specs = [_Slot(name, t.dtype, tuple(t.shape), off, n) for (name, t), off, n in zip(tensors, offsets, sizes)]
+        end = specs[-1].offset + _padded(specs[-1].nbytes)
+        return cls(fmt, qt._layout_cls, type(qt._params), fields, specs, max(end, ALIGN), source)
 
-# ------------------------------------------------------------ QuantizedWeight <-> bytes
+    def check(self, tensors, fields):
+        """RuntimeError when a weight's components or parameters differ from the planned ones."""
+        layout = [(name, t.dtype, tuple(t.shape)) for name, t in tensors]
+        if layout != [(n, d, tuple(s)) for n, d, s, _, _ in self.specs]:
+            raise RuntimeError(f"Layout of {self.fmt} differs from the template: {layout}")
+        differ = {k: (fields.get(k), self.fields.get(k)) for k in fields.keys() | self.fields.keys()
+                  if not _same_param(fields.get(k), self.fields.get(k))}
+        if differ or fields.keys() != self.fields.keys():
+            raise RuntimeError(f"Parameters of {self.fmt} differ from the template (the data would decode "
+                               f"wrongly): {differ}")
+
+    def to_bytes(self, tensors, device):
+        """The byte vector: every component at its offset, zero padding between and after."""
+        pieces = []
+        for (_, tensor), slot in zip(tensors, self.specs):
+            pieces.append(_byte_view(tensor).to(device))
+            gap = _padded(slot.nbytes) - slot.nbytes
+            if gap:
+                pieces.append(torch.zeros(gap, dtype=torch.uint8, device=device))
+        out = torch.cat(pieces)
+        if out.numel() < self.total:
+            out = torch.cat([out, torch.zeros(self.total - out.numel(), dtype=torch.uint8, device=device)])
+        return out
+
+    def views(self, full):
+        """{name: zero-copy view of its component in `full`}."""
+        return {n: full.narrow(0, o, b).view(d).view(s) for n, d, s, o, b in self.specs}
+
+
+def _same_param(a, b):
+    """Equal parameter values; the dtype field (orig_dtype) is set at unpack and never compared."""
+    if isinstance(a, torch.dtype) or isinstance(b, torch.dtype):
+        return True
+    if isinstance(a, (tuple, list)) and isinstance(b, (tuple, list)):
+        return list(a) == list(b)
+    return a == b
+
+
 def comfy_quant():
     """The module holding QuantizedWeight / QUANT_ALGOS (ComfyUI's comfy.quant_ops in the reference)."""
     return qtm
@@ -69,75 +138,39 @@ def layout_name(fmt):
 
 
 def components(qt, extras=None):
-    """(tensors in byte-vector order, non-tensor fields)."""
-    tensors, fields = [("_qdata", qt._qdata)], {}
-    for field in dataclasses.fields(qt._params):
-        value = getattr(qt._params, field.name)
-        if isinstance(value, torch.Tensor):
-            tensors.append((field.name, value))
-        else:
-            fields[field.name] = value
-    for name, value in sorted((extras or {}).items()):
-        tensors.append(("x:" + name, value))
-    return tensors, fields
-
-
-def _same_field(a, b):
-    if isinstance(a, torch.dtype) or isinstance(b, torch.dtype):
-        return True  # orig_dtype is set by unpack
-    if isinstance(a, (tuple, list)) or isinstance(b, (tuple, list)):
-        return tuple(a) == tuple(b)
-    return a == b
+    """(tensors in byte-vector order, non-tensor fields): _qdata, the params' tensor fields in
+    declaration order, then the extras by name as "x:<name>"."""
+    values = {f.name: getattr(qt._params, f.name) for f in dataclasses.fields(qt._params)}
+    tensors = [("_qdata", qt._qdata)]
+    tensors += [(k, v) for k, v in values.items() if isinstance(v, torch.Tensor)]
+    tensors += [("x:" + k, (extras or {})[k]) for k in sorted(extras or {})]
+    return tensors, {k: v for k, v in values.items() if not isinstance(v, torch.Tensor)}
 
 
 def plan_from_quantized(qt, fmt, source, extras=None):
-    tensors, fields = components(qt, extras)
-    specs, offset = [], 0
-    for name, tensor in tensors:
-        nbytes = tensor.numel() * tensor.element_size()
-        specs.append((name, tensor.dtype, tuple(tensor.shape), offset, nbytes))
-        offset += math.ceil(nbytes / ALIGN) * ALIGN
-    return QuantPlan(fmt, qt._layout_cls, type(qt._params), fields, specs, max(offset, ALIGN), source)
+    return QuantPlan.of(qt, fmt, source, extras)
 
 
 def pack(qt, plan, device, extras=None):
     """One uint8 vector [plan.total] holding every component at its aligned offset."""
     tensors, fields = components(qt, extras)
-    got = [(n, t.dtype, tuple(t.shape)) for n, t in tensors]
-    if got != [(n, d, s) for n, d, s, _, _ in plan.specs]:
-        raise RuntimeError(f"Layout of {plan.fmt} differs from the template: {got}")
-    differ = {k: (v, plan.fields.get(k)) for k, v in fields.items() if not _same_field(v, plan.fields.get(k))}
-    if differ or fields.keys() != plan.fields.keys():
-        raise RuntimeError(f"Parameters of {plan.fmt} differ from the template (the data would decode wrongly): {differ}")
-    out = torch.zeros(plan.total, dtype=torch.uint8, device=device)
-    for (name, tensor), (_, _, _, offset, nbytes) in zip(tensors, plan.specs):
-        out[offset:offset + nbytes].copy_(tensor.detach().contiguous().reshape(-1).view(torch.uint8).to(device))
-    return out
+    plan.check(tensors, fields)
+    return plan.to_bytes(tensors, device)
 
 
 def unpack(full, plan, dtype=None, with_extras=False):
     """Gathered byte vector -> QuantizedWeight of zero-copy views [+ extras]."""
-    values, extras = {}, {}
-    for name, tensor_dtype, shape, offset, nbytes in plan.specs:
-        view = full[offset:offset + nbytes].view(tensor_dtype).reshape(shape)
-        if name.startswith("x:"):
-            extras[name[2:]] = view
-        else:
-            values[name] = view
+    views = plan.views(full)
+    extras = {name[2:]: v for name, v in views.items() if name.startswith("x:")}
+    tensor_fields = {name: v for name, v in views.items() if name != "_qdata" and not name.startswith("x:")}
     fields = dict(plan.fields)
     if dtype is not None and "orig_dtype" in fields:
         fields["orig_dtype"] = dtype
-    params = plan.params_cls(**fields, **{k: v for k, v in values.items() if k != "_qdata"})
-    qt = qtm.QuantizedWeight(values["_qdata"], plan.layout, params)
+    qt = qtm.QuantizedWeight(views["_qdata"], plan.layout, plan.params_cls(**tensor_fields, **fields))
     return (qt, extras) if with_extras else qt
 
 
 # ------------------------------------------------------------------- file formats
-def _conf_param(conf, name, default):
-    params = conf.get("params") if isinstance(conf.get("params"), dict) else {}
-    return conf.get(name, params.get(name, default))
-
-
 def quantized_from_file(handle, entries, module, conf, shape, device, dtype, meta=False):
     """QuantizedWeight from a module's file tensors.
 
@@ -162,11 +195,9 @@ def quantized_from_file(handle, entries, module, conf, shape, device, dtype, met
         scale = state.get(prefix + "weight_scale")
         if weight.dtype != torch.int8 or scale is None or scale.numel() != n:
             raise ValueError(f"{module}: int8_tensorwise expects I8 [N, K] weight and F32 [N, 1] weight_scale")
-        convrot = bool(_conf_param(conf, "convrot", False))
-        group = int(_conf_param(conf, "convrot_groupsize", 256))
-        if convrot and (group < 4 or group & (group - 1) or (group.bit_length() - 1) % 2 or k % group):
-            raise ValueError(f"{module}: invalid ConvRot group {group}")
-        params = qtm.Int8RowwiseParams(scale.to(dev, torch.float32).reshape(n, 1), dtype, convrot, group)
+        rot = qf.convrot_config(conf, k, module)
+        params = qtm.Int8RowwiseParams(scale.to(dev, torch.float32).reshape(n, 1), dtype, rot["convrot"],
+                                       rot["group_size"])
         return qtm.QuantizedWeight(weight.to(dev), qtm.Int8RowwiseLayout, params)
     if fmt == "float8_e4m3fn":
         scale = state.get(prefix + "weight_scale", state.get(prefix + "scale_weight"))
@@ -177,7 +208,7 @@ def quantized_from_file(handle, entries, module, conf, shape, device, dtype, met
         return qtm.QuantizedWeight(weight.to(dev), qtm.Float8ScaledLayout, qtm.Float8ScaledParams(scale, dtype))
     if fmt == "int4_asym_group":
         scale, zero = state.get(prefix + "weight_scale"), state.get(prefix + "weight_zero")
-        group = int(_conf_param(conf, "group_size", 128))
+        group = int(qf.conf_value(conf, "group_size", 128))
         if (weight.dtype != torch.uint8 or tuple(weight.shape) != (n, k // 2) or scale is None or zero is None
                 or k % group or tuple(scale.shape) != (n, k // group) or tuple(zero.shape) != (n, k // group)):
             raise ValueError(f"{module}: int4_asym_group expects U8 [N, K/2] weight and F16 [N, K/g] scale/zero")
@@ -192,15 +223,17 @@ def quantized_from_float(weight, fmt, **options):
 
 
 def requantize_like(template, weight, fmt):
-    """New weight (after LoRA) in the template's layout; ConvRot / group options are kept."""
-    if hasattr(template, "requantize_from_float"):
-        return template.requantize_from_float(weight, scale="recalculate")
-    return quantized_from_float(weight, fmt)
+    """A new weight (after LoRA) in the template's layout: its ConvRot / group options carry over."""
+    again = getattr(template, "requantize_from_float", None)
+    return quantized_from_float(weight, fmt) if again is None else again(weight, scale="recalculate")
 
 
 # ------------------------------------------------------------------------- module
 class QuantLinear(nn.Module):
     """Linear whose weight is one QuantizedWeight byte vector (FSDP Shard(0) over bytes)."""
+
+    # attributes the FP16-safe / finite-tracking machinery set on the Linear it replaces
+    CARRIED = ("_ps_tracker", "_ps_finite_slot", "_ps_safe", "_ps_fp32")
 
     def __init__(self, src, plan, compute_dtype, native, follow_input=False, full_precision=False):
         super().__init__()
@@ -212,7 +245,7 @@ class QuantLinear(nn.Module):
         self._ps_native = native
         self._ps_follow_input = follow_input
         self._ps_full_precision = full_precision  # comfy_quant full_precision_matrix_mult: dequantize only
-        for attr in ("_ps_tracker", "_ps_finite_slot", "_ps_safe", "_ps_fp32"):
+        for attr in self.CARRIED:
             if hasattr(src, attr):
                 setattr(self, attr, getattr(src, attr))
 
@@ -248,48 +281,61 @@ class QuantLinear(nn.Module):
             raise ValueError(f"silu_gate needs an even number of output features, got {self.out_features}")
         return self._forward(x, activation)
 
-    def _forward(self, x, activation):
-        plan = self._ps_qplan
-        shape = x.shape
-        if self._ps_follow_input and not self._ps_native:
-            dtype = x.dtype if x.is_floating_point() else self._ps_compute_dtype
-        else:
-            dtype = self._ps_compute_dtype
-        rows = x.reshape(-1, shape[-1]).to(dtype)
-        bias = None if self.bias is None else self.bias.to(dtype)
-        qt, extras = unpack(self.qbytes, plan, dtype, with_extras=True)
-        pre = extras.get("pre_quant_scale")
-        if pre is not None:  # ModelOpt AWQ smoothing
-            rows = rows * pre.to(rows.dtype)
-        # The reference's V100 "FP16 safe" mode computes the dequantized GEMM with an FP32 result.
-        safe = getattr(self, "_ps_safe", False) and dtype == torch.float16
-        out = None
-        fused = False   # activation applied by native_linear
-        if self._ps_native and not safe and not self._ps_full_precision:
-            # the fused gate pairs 64-column blocks: other widths take the gate as a separate pass
-            native_act = None if activation == "silu_gate" and self.out_features % 128 else activation
-            try:
-                out = native_linear(rows, qt, bias, plan.fmt, extras.get("input_scale"), native_act)
-                fused = native_act is not None
-            except torch.cuda.OutOfMemoryError:
-                raise
-            except (NotImplementedError, RuntimeError, TypeError, ValueError) as error:
-                warnings.warn(f"PowerShard: native {plan.fmt} GEMM unavailable ({error}); the module switches to dequantize")
-                self._ps_native = False
-                out = None
-        if out is None and safe:
-            out = F.linear(rows.float(), qt.dequantize().float(), None if bias is None else bias.float())
-        elif out is None:
-            out = F.linear(rows, qt.dequantize().to(dtype), bias)
-        if activation is not None and not fused:
-            out = apply_activation(out, activation)
-        out = out.reshape(shape[:-1] + (out.shape[-1],))
+    # -- the forward in four steps: compute dtype, the native attempt, the dequantize branch, delivery
+    def _dtype_for(self, x):
+        """The compute dtype; a dequantizing text-encoder module follows a floating input instead."""
+        if self._ps_follow_input and not self._ps_native and x.is_floating_point():
+            return x.dtype
+        return self._ps_compute_dtype
+
+    def _native_attempt(self, rows, qt, bias, extras, activation):
+        """(output, activation applied) from the native kernels, or (None, False) to dequantize:
+        the FP16-safe mode and full-precision files never go native, and a native failure switches
+        the module to dequantize for good with one warning."""
+        safe = getattr(self, "_ps_safe", False) and rows.dtype == torch.float16
+        if not self._ps_native or safe or self._ps_full_precision:
+            return None, False
+        # the fused gate pairs 64-column blocks: other widths take the gate as a separate pass
+        act = None if activation == "silu_gate" and self.out_features % 128 else activation
+        try:
+            return native_linear(rows, qt, bias, self._ps_qplan.fmt, extras.get("input_scale"), act), act is not None
+        except torch.cuda.OutOfMemoryError:
+            raise
+        except NATIVE_FAILURES as error:
+            warnings.warn(f"PowerShard: native {self._ps_qplan.fmt} GEMM unavailable ({error}); the module "
+                          f"switches to dequantize")
+            self._ps_native = False
+            return None, False
+
+    def _dequantized(self, rows, qt, bias):
+        """F.linear on the dequantized weight; the V100 "FP16 safe" mode computes it in fp32."""
+        if getattr(self, "_ps_safe", False) and rows.dtype == torch.float16:
+            return F.linear(rows.float(), qt.dequantize().float(), None if bias is None else bias.float())
+        return F.linear(rows, qt.dequantize().to(rows.dtype), bias)
+
+    def _deliver(self, out, x):
+        out = out.reshape(*x.shape[:-1], out.shape[-1])
         if self._ps_follow_input and x.is_floating_point() and out.dtype != x.dtype:
             out = out.to(x.dtype)  # text encoder: the FP32 graph is not narrowed to bf16 by the native kernel
         tracker = getattr(self, "_ps_tracker", None)
         if tracker is not None:
             tracker.observe(self._ps_finite_slot, out)
         return out
+
+    def _forward(self, x, activation):
+        dtype = self._dtype_for(x)
+        qt, extras = unpack(self.qbytes, self._ps_qplan, dtype, with_extras=True)
+        rows = x.reshape(-1, x.shape[-1]).to(dtype)
+        pre = extras.get("pre_quant_scale")
+        if pre is not None:  # ModelOpt AWQ smoothing
+            rows = rows * pre.to(rows.dtype)
+        bias = None if self.bias is None else self.bias.to(dtype)
+        out, applied = self._native_attempt(rows, qt, bias, extras, activation)
+        if out is None:
+            out = self._dequantized(rows, qt, bias)
+        if activation is not None and not applied:
+            out = apply_activation(out, activation)
+        return self._deliver(out, x)
 
 
 # ------------------------------------------------------------------ shared activation quantization
@@ -400,16 +446,111 @@ UNSUPPORTED_TARGETS = ("mxfp8", "nvfp4")
 
 
 def is_linear(module):
+    """nn.Linear, or a Linear-like module (in_features and a 2-D weight Parameter)."""
+    if isinstance(module, nn.Linear):
+        return True
     weight = getattr(module, "weight", None)
-    return isinstance(module, nn.Linear) or (hasattr(module, "in_features") and isinstance(weight, nn.Parameter)
-                                             and weight.ndim == 2)
+    return hasattr(module, "in_features") and isinstance(weight, nn.Parameter) and weight.ndim == 2
 
 
 def fits_blocks(module, fmt):
-    k, n = module.in_features, module.out_features
-    if fmt == "int4_asym_group":
-        return k % 128 == 0 and n >= 16
-    return n >= 16
+    """Whether the format's blocks fit the layer: 16 output features at least, and for the uint4
+    groups an input width that holds whole 128-element groups."""
+    if module.out_features < 16:
+        return False
+    return fmt != "int4_asym_group" or module.in_features % 128 == 0
+
+
+class _Installer:
+    """One install_quant_linears pass: picks the eligible Linears, decides their stored format and
+    source, shares one weight template per layout signature and one native decision per format,
+    swaps in the QuantLinear modules and builds the report."""
+
+    def __init__(self, tensors, weight_format, compute, scope, compute_dtype, device, name_map, follow_input,
+                 quant_options):
+        self.tensors, self.weight_format, self.compute = tensors, weight_format, compute
+        self.scope, self.compute_dtype, self.device = scope, compute_dtype, device
+        self.name_map, self.follow_input, self.options = name_map, follow_input, quant_options or {}
+        self.templates, self.natives = {}, {}
+        self.report = dict(weight_format=weight_format, compute=compute, modules={}, skipped=0, stored_bytes=0)
+
+    def eligible(self, name, module):
+        if not is_linear(module) or isinstance(module, QuantLinear) or getattr(module, "_ps_fp32", False):
+            return False
+        weight = getattr(module, "weight", None)
+        if weight is not None and weight.dtype == torch.float32:
+            return False   # FP32 islands (AdaLN / timestep / caption) stay unquantized
+        return not self.scope or name.startswith(tuple(self.scope))
+
+    def locate(self, name):
+        """(table, weight key, its description) of a module's weight, or None without one."""
+        table, key = self.name_map(name + ".weight") if self.name_map else (self.tensors, name + ".weight")
+        desc = table.get(key) if table is not None else None
+        return None if desc is None else (table, key, desc)
+
+    def stored_format(self, desc):
+        """(format, "file" | "quantize") or None when the module stays as it is."""
+        record = desc.get("comfy_quant")
+        if self.weight_format == "as_file":
+            return None if record is None else (record["format"], "file")
+        fmt = TARGETS[self.weight_format]
+        return fmt, "file" if record is not None and record.get("format") == fmt else "quantize"
+
+    def file_template(self, table, key, desc, fmt, shape):
+        module = key[:-len(".weight")]
+        own = {n: (getattr(torch, SAFETENSORS_DTYPES[d["dtype"]]), d.get("stored_shape", d["shape"]))
+               for n, d in _module_tensors(table, module).items()}
+        extras = {x: torch.empty(own[module + "." + x][1], dtype=own[module + "." + x][0], device="meta")
+                  for x in EXTRAS if module + "." + x in own}
+        signature = ("file", fmt, json_key(desc["comfy_quant"]), tuple(shape),
+                     tuple((n[len(module):], str(dt), tuple(sh)) for n, (dt, sh) in sorted(own.items())))
+        if signature not in self.templates:
+            self.templates[signature] = quantized_from_file(None, own, module, desc["comfy_quant"], shape,
+                                                            self.device, self.compute_dtype, meta=True)
+        source = dict(kind="file", table=table, module=module, conf=desc["comfy_quant"], key=key)
+        return self.templates[signature], source, extras
+
+    def quantize_template(self, table, key, fmt, shape):
+        signature = ("quantize", fmt, tuple(shape))
+        if signature not in self.templates:
+            self.templates[signature] = _template_from_shape(
+                torch.empty(shape, dtype=self.compute_dtype, device="meta"), fmt, self.options)
+        return self.templates[signature], dict(kind="quantize", table=table, module=key[:-len(".weight")], key=key)
+
+    def native(self, fmt):
+        if fmt not in self.natives:
+            self.natives[fmt] = {"native": (True, "native selected"),
+                                 "dequantize": (False, "dequantize selected")}.get(self.compute) \
+                or native_support(fmt, torch.device(self.device))
+        return self.natives[fmt]
+
+    def install(self, net, name, module):
+        found = self.locate(name)
+        if found is None:
+            return
+        table, key, desc = found
+        chosen = self.stored_format(desc)
+        if chosen is None:
+            return
+        fmt, kind = chosen
+        if not fits_blocks(module, fmt):
+            self.report["skipped"] += 1
+            return
+        shape = [module.out_features, module.in_features]
+        if kind == "file":
+            qt, source, extras = self.file_template(table, key, desc, fmt, shape)
+        else:
+            (qt, source), extras = self.quantize_template(table, key, fmt, shape), None
+        plan = plan_from_quantized(qt, fmt, source, extras)
+        native, reason = self.native(fmt)
+        full_precision = kind == "file" and bool(desc["comfy_quant"].get("full_precision_matrix_mult"))
+        parent, _, leaf = name.rpartition(".")
+        owner = net.get_submodule(parent) if parent else net
+        setattr(owner, leaf, QuantLinear(module, plan, self.compute_dtype, native, self.follow_input, full_precision))
+        entry = self.report["modules"].setdefault(fmt, dict(count=0, native=native, reason=reason, source={}))
+        entry["count"] += 1
+        entry["source"][kind] = entry["source"].get(kind, 0) + 1
+        self.report["stored_bytes"] += plan.total
 
 
 def install_quant_linears(net, tensors, weight_format, compute, scope, compute_dtype, device, open_file=None,
@@ -419,76 +560,24 @@ def install_quant_linears(net, tensors, weight_format, compute, scope, compute_d
     name_map: parameter name -> (table, name in table) for multi-file models.
     quant_options (this package's addition): layout options of quantize-at-load weights, e.g.
     {"convrot": True, "convrot_groupsize": 256} for int8 or {"group_size": 128} for int4.
+    open_file is accepted for the reference's signature; every template here is built from shapes.
     Returns a report.
     """
-    report = dict(weight_format=weight_format, compute=compute, modules={}, skipped=0, stored_bytes=0)
-    if weight_format == "dequantize":
-        return report
     if weight_format in UNSUPPORTED_TARGETS:
         raise ValueError(f"weight_format {weight_format} is a Blackwell block format, not supported on MI355X")
-    templates, natives = {}, {}
-    for name, module in list(net.named_modules()):
-        if not is_linear(module) or getattr(module, "_ps_fp32", False) or isinstance(module, QuantLinear):
-            continue
-        if getattr(module, "weight", None) is not None and module.weight.dtype == torch.float32:
-            continue  # FP32 islands (AdaLN / timestep / caption) stay unquantized
-        if scope and not any(name.startswith(s) for s in scope):
-            continue
-        table, key = (name_map(name + ".weight") if name_map else (tensors, name + ".weight"))
-        desc = table.get(key) if table is not None else None
-        if desc is None:
-            continue
-        file_conf = desc.get("comfy_quant")
-        if weight_format == "as_file":
-            if file_conf is None:
-                continue
-            fmt, kind = file_conf["format"], "file"
-        else:
-            fmt = TARGETS[weight_format]
-            kind = "file" if file_conf is not None and file_conf.get("format") == fmt else "quantize"
-        if not fits_blocks(module, fmt):
-            report["skipped"] += 1
-            continue
-        module_key = key[:-len(".weight")]
-        shape = [module.out_features, module.in_features]
-        extras = None
-        if kind == "file":
-            entries = {n: (getattr(torch, _torch_dtype(d["dtype"])), d.get("stored_shape", d["shape"]))
-                       for n, d in _entries(table, module_key).items()}
-            extras = {x: torch.empty(entries[module_key + "." + x][1], dtype=entries[module_key + "." + x][0],
-                                     device="meta") for x in EXTRAS if module_key + "." + x in entries}
-            signature = ("file", fmt, json_key(file_conf), tuple(shape),
-                         tuple((n[len(module_key):], str(v[0]), tuple(v[1])) for n, v in sorted(entries.items())))
-            if signature not in templates:
-                templates[signature] = quantized_from_file(None, entries, module_key, file_conf, shape, device,
-                                                           compute_dtype, meta=True)
-            qt = templates[signature]
-            source = dict(kind="file", table=table, module=module_key, conf=file_conf, key=key)
-        else:
-            signature = ("quantize", fmt, tuple(shape))
-            if signature not in templates:
-                dummy = torch.ones(shape, dtype=compute_dtype, device="meta")
-                templates[signature] = _template_from_shape(dummy, fmt, quant_options or {})
-            qt = templates[signature]
-            source = dict(kind="quantize", table=table, module=module_key, key=key)
-        plan = plan_from_quantized(qt, fmt, source, extras)
-        if fmt not in natives:
-            if compute == "native":
-                natives[fmt] = (True, "native selected")
-            elif compute == "dequantize":
-                natives[fmt] = (False, "dequantize selected")
-            else:
-                natives[fmt] = native_support(fmt, torch.device(device))
-        parent_name, _, leaf = name.rpartition(".")
-        parent = net.get_submodule(parent_name) if parent_name else net
-        full_precision = bool(kind == "file" and file_conf.get("full_precision_matrix_mult"))
-        setattr(parent, leaf, QuantLinear(module, plan, compute_dtype, natives[fmt][0], follow_input, full_precision))
-        entry = report["modules"].setdefault(fmt, dict(count=0, native=natives[fmt][0], reason=natives[fmt][1],
-                                                      source={}))
-        entry["count"] += 1
-        entry["source"][kind] = entry["source"].get(kind, 0) + 1
-        report["stored_bytes"] += plan.total
-    return report
+    installer = _Installer(tensors, weight_format, compute, scope, compute_dtype, device, name_map, follow_input,
+                           quant_options)
+    if weight_format != "dequantize":
+        for name, module in list(net.named_modules()):
+            if installer.eligible(name, module):
+                installer.install(net, name, module)
+    return installer.report
+
+
+def _convrot_options(options, k):
+    rot = qf.convrot_config({"convrot": options.get("convrot", False),
+                             "convrot_groupsize": options.get("convrot_groupsize", 256)}, k, "in_features")
+    return rot["convrot"], rot["group_size"]
 
 
 def _template_from_shape(weight_meta, fmt, options):
@@ -497,10 +586,7 @@ def _template_from_shape(weight_meta, fmt, options):
     dtype = weight_meta.dtype
     meta = torch.device("meta")
     if fmt == "int8_tensorwise":
-        convrot = bool(options.get("convrot", False))
-        group = int(options.get("convrot_groupsize", 256))
-        if convrot and (group < 4 or group & (group - 1) or (group.bit_length() - 1) % 2 or k % group):
-            raise ValueError(f"invalid ConvRot group {group} for in_features {k}")
+        convrot, group = _convrot_options(options, k)
         params = qtm.Int8RowwiseParams(torch.empty(n, 1, dtype=torch.float32, device=meta), dtype, convrot, group)
         return qtm.QuantizedWeight(torch.empty(n, k, dtype=torch.int8, device=meta), qtm.Int8RowwiseLayout, params)
     if fmt == "float8_e4m3fn":
@@ -521,11 +607,9 @@ def json_key(conf):
     return json.dumps(conf, sort_keys=True)
 
 
-def _entries(table, module):
-    prefix = module + "."
-    return {n: d for n, d in table.items()
-            if n.startswith(prefix) and "." not in n[len(prefix):] and not n.endswith(".bias")
-            and not n.endswith(".comfy_quant")}
+def _module_tensors(table, module):
+    """A module's own file tensors (weight, scales, zero, extras): no bias, no comfy_quant record."""
+    return qf.QuantHeader(table).own(module, with_record=False)
 
 
 # safetensors dtype code -> torch dtype attribute name
@@ -539,64 +623,93 @@ def _torch_dtype(code):
 
 
 # ------------------------------------------------------------------------ loading
+# the scale tensors that accompany a plain fp8 weight, in the order they are looked up
+_FP8_SCALE_SUFFIXES = (".scale_weight", ".weight_scale")
+
+
+def _fp8_scale(handle, table, module, device):
+    """The first float scale beside a plain fp8 weight (per tensor, or per row as [N, 1]); None if
+    there is none."""
+    for suffix in _FP8_SCALE_SUFFIXES:
+        desc = table.get(module + suffix)
+        if desc is not None and desc["dtype"] in ("F32", "F16", "BF16"):
+            value = handle.get_tensor(desc["key"]).float().to(device)
+            return value.reshape(-1, 1) if value.numel() > 1 else value.reshape(())
+    return None
+
+
 def float_weight(handle, table, key, device, dtype=torch.float32):
     """A module's full weight as float: plain / fp8 (+scale) / comfy_quant (dequantized here)."""
-    from .quant_formats import dequantize_module, module_entries
     desc = table[key]
     module = key[:-len(".weight")]
     if desc.get("comfy_quant") is not None:
-        return dequantize_module(handle, module_entries(table, module), module, desc["comfy_quant"], desc["shape"],
-                                 device, dtype)
+        return qf.dequantize_module(handle, qf.module_entries(table, module), module, desc["comfy_quant"],
+                                    desc["shape"], device, dtype)
     weight = handle.get_tensor(desc["key"]).to(device)
     if desc["dtype"] in ("F8_E4M3", "F8_E5M2"):
         weight = weight.float()
-        for suffix in (".scale_weight", ".weight_scale"):
-            scale = table.get(module + suffix)
-            if scale is not None and scale["dtype"] in ("F32", "F16", "BF16"):
-                value = handle.get_tensor(scale["key"]).float().to(device)
-                weight = weight * (value.reshape(-1, 1) if value.numel() > 1 else value.reshape(()))
-                break
+        scale = _fp8_scale(handle, table, module, device)
+        if scale is not None:
+            weight = weight * scale
     return weight.to(dtype)
+
+
+def _used_names(table, module, key, kind):
+    """The table entries a module's bytes are built from."""
+    used = set(_module_tensors(table, module)) | {key}
+    if module + qf.QUANT_SUFFIX in table:
+        used.add(module + qf.QUANT_SUFFIX)
+    if kind != "file":
+        used |= {module + s for s in _FP8_SCALE_SUFFIXES if module + s in table}
+    return used
+
+
+def _checked_finite(weight, key, when):
+    if not torch.isfinite(weight).all():
+        raise FloatingPointError(f"{key}: non-finite weights {when}")
+    return weight
+
+
+def _file_weight(handle, plan, shape, device, dtype, delta):
+    """(QuantizedWeight, extras) of a file module; a LoRA delta is added to the true weight
+    W = Wq * pre_quant_scale (per input), i.e. delta / s in Wq space, and the sum requantized in the
+    file's layout."""
+    src = plan.source
+    table, module = src["table"], src["module"]
+    files = {n: d["key"] for n, d in _module_tensors(table, module).items()}
+    qt = quantized_from_file(handle, files, module, src["conf"], shape, device, dtype)
+    extras = {x: handle.get_tensor(table[module + "." + x]["key"]).to(device) for x in EXTRAS
+              if module + "." + x in table}
+    if delta is not None:
+        pre = extras.get("pre_quant_scale")
+        step = delta.float() if pre is None else delta.float() / pre.float().reshape(1, -1)
+        weight = _checked_finite(qt.dequantize().float() + step, src["key"], "after LoRA")
+        qt = requantize_like(qt, weight.to(dtype), plan.fmt)
+    return qt, extras
+
+
+def _quantized_at_load(handle, plan, device, dtype, delta):
+    """QuantizedWeight of a float (or fp8-scaled) file weight quantized into the planned layout."""
+    src = plan.source
+    weight = float_weight(handle, src["table"], src["key"], device)
+    if delta is not None:
+        weight = weight + delta
+    weight = _checked_finite(weight, src["key"], "before quantization")
+    return quantized_from_float(weight.to(dtype), plan.fmt, **_quantize_options(plan))
 
 
 def build_bytes(module, handle, device, lora_delta=None):
     """The full QuantLinear byte vector on device; returns (bytes, table names used)."""
     plan = module._ps_qplan
-    source = plan.source
-    table, key, name = source["table"], source["key"], source["module"]
-    used = set(_entries(table, name)) | {key}
-    if name + ".comfy_quant" in table:
-        used.add(name + ".comfy_quant")
-    dtype = module._ps_compute_dtype
+    src = plan.source
     shape = [module.out_features, module.in_features]
-    delta = lora_delta(key, shape, device) if lora_delta else None
-    extras = None
-    if source["kind"] == "file":
-        entries = {n: d["key"] for n, d in _entries(table, name).items()}
-        qt = quantized_from_file(handle, entries, name, source["conf"], shape, device, dtype)
-        extras = {x: handle.get_tensor(table[name + "." + x]["key"]).to(device) for x in EXTRAS
-                  if name + "." + x in table}
-        if delta is not None:
-            # LoRA on the true weight W = Wq * pre_quant_scale (per input): delta / s in Wq space.
-            weight = qt.dequantize().float()
-            pre = extras.get("pre_quant_scale")
-            weight = weight + (delta.float() / pre.float().reshape(1, -1) if pre is not None else delta.float())
-            if not torch.isfinite(weight).all():
-                raise FloatingPointError(f"{key}: non-finite weights after LoRA")
-            qt = requantize_like(qt, weight.to(dtype), plan.fmt)
-            del weight
+    delta = lora_delta(src["key"], shape, device) if lora_delta else None
+    dtype = module._ps_compute_dtype
+    if src["kind"] == "file":
+        qt, extras = _file_weight(handle, plan, shape, device, dtype, delta)
     else:
-        weight = float_weight(handle, table, key, device)
-        for suffix in (".scale_weight", ".weight_scale"):
-            if name + suffix in table:
-                used.add(name + suffix)
-        if delta is not None:
-            weight = weight + delta
-        if not torch.isfinite(weight).all():
-            raise FloatingPointError(f"{key}: non-finite weights before quantization")
-        qt = quantized_from_float(weight.to(dtype), plan.fmt, **_quantize_options(plan))
-        del weight
-    return pack(qt, plan, device, extras), used
+        qt, extras = _quantized_at_load(handle, plan, device, dtype, delta), None
+    return pack(qt, plan, device, extras), _used_names(src["table"], src["module"], src["key"], src["kind"])
 
 
 def _quantize_options(plan):
