@@ -751,6 +751,180 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     }
 }
 
+// ------------------------------------------------------ uint4 decode kernel (M <= 4)
+// Decode shapes (a few tokens against the whole weight).  A workgroup of 8 waves owns 128 weight
+// rows, 16 per wave, over the whole K, as in the streaming kernel above, but the waves never
+// meet after the start:
+//  * the activations (M rows, at most a few tens of KB) are loaded into LDS once, behind one
+//    barrier;
+//  * each wave streams its own 16 rows (2 KB of nibbles per 256-k block) and their scales and zeros
+//    through a private LDS ring of D blocks that it alone fills and reads, so a block is ready when
+//    the wave's own load counter says so -- no barrier per block, and no wave waits for another.
+// The arithmetic is the streaming kernel's (w = round_16(fmaf(q, s, -z s)), 16x16x32 MFMA with the
+// activations as the A operand, lane group h carrying k = 64 h + 8 t of the block in k-step t).
+namespace wd {
+constexpr int NW = 8, ROWS = 16 * NW;                 // waves; weight rows per workgroup
+constexpr int B = 256;                                // k per block
+constexpr int WBYTES = 16 * B / 2;                    // a wave's nibbles per block (2 KB)
+constexpr int WSLOT = WBYTES + 256;                   // + its scale / zero words
+constexpr int MAXM = 4;
+constexpr int LOADS = 3;                              // ring loads per wave and block
+__host__ __device__ inline int64_t xrow(int64_t K) { return 2 * K + 16; } // padded activation row in LDS (bytes)
+inline int64_t lds_bytes(int64_t M, int64_t K, int D) { return M * xrow(K) + (int64_t)NW * D * WSLOT; }
+}  // namespace wd
+
+template <int XDT, int D>
+__global__ void __launch_bounds__(wd::NW * 64)
+gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
+{
+    using namespace wd;
+    using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nr = lane & 15, h = lane >> 4;
+    const int nb = K / B, G = K / wa.gs, hg = wa.gs / 128;
+    const int64_t wld = K / 2, xr = xrow(K);
+    const int row0 = blockIdx.x * ROWS + 16 * wave;
+    uint8_t *const ring = smem + (int64_t)M * xr + (int64_t)wave * D * WSLOT;
+
+    // the activations: row m at m * xr, 1 KB per wave load (K % 512 == 0: whole loads per row)
+    const int per_row = (int)(2 * (int64_t)K / 1024), nx = M * per_row;
+    for (int j = wave; j < nx; j += NW) {
+        const int m = j / per_row, c = j - m * per_row;
+        __builtin_amdgcn_global_load_lds((glb_ptr)((const uint8_t *)x + (int64_t)m * ldx * 2 + c * 1024 + lane * 16),
+                                         (lds_ptr)(smem + (int64_t)m * xr + c * 1024), 16, 0, 0);
+    }
+    // a block's ring loads (past the end: the last block again, into a slot nobody reads)
+    uint32_t wo[2];
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        const int r = 8 * d + lane / 8, pc = lane % 8;
+        wo[d] = (uint32_t)(min(row0 + r, N - 1) * wld + (pc ^ ((r >> 1) & 7)) * 16);
+    }
+    const bool szhi = (lane & 1) != 0;
+    const uint16_t *const szrow = (lane < 32 ? wa.scale16 : wa.zero16) + (int64_t)min(row0 + ((lane >> 1) & 15), N - 1) * G;
+    // blocks are issued in order; the group of half 2 b is kept as a running quotient gq and
+    // remainder gr of 2 b by hg on the scalar unit (no per-lane division)
+    int gq = 0, gr = 0;
+    auto issue = [&](int b, int slot) {
+        const int bc = min(b, nb - 1);
+        uint8_t *const sl = ring + slot * WSLOT;
+        const uint8_t *const wb = wa.wq + (int64_t)bc * (B / 2);
+#pragma unroll
+        for (int d = 0; d < 2; d++)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(wb + wo[d]), (lds_ptr)(sl + 1024 * d), 16, 0, 0);
+        const int g = min(gq + (szhi && gr + 1 >= hg ? 1 : 0), G - 1);   // group of the lane's 128-k half
+        __builtin_amdgcn_global_load_lds((glb_ptr)(szrow + g), (lds_ptr)(sl + WBYTES), 2, 0, 0);
+        gr += 2;
+        if (gr >= hg) { gr -= hg; gq++; }
+        if (gr >= hg) { gr -= hg; gq++; }
+    };
+#pragma unroll
+    for (int b = 0; b < D; b++) issue(b, b);
+    wait_vmcnt<LOADS * D>();            // this wave's activation loads (issued first) landed
+    stage_barrier();                    // ... and every other wave's
+
+    struct Ops { XV xf[8]; v4i wv[2]; float sc, zs; };
+    const uint8_t *const xrow_p = smem + (int64_t)min(nr, M - 1) * xr;
+    auto read = [&](int b, int slot, Ops &o) {
+        const uint8_t *const sl = ring + slot * WSLOT;
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+            o.xf[t] = __builtin_bit_cast(XV, *(const v4i *)(xrow_p + ((int64_t)b * B + 64 * h + 8 * t) * 2));
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = 2 * h + i;
+            o.wv[i] = *(const v4i *)(sl + nr * (B / 2) + ((c ^ ((nr >> 1) & 7)) << 4));
+        }
+        const int si = (nr << 1) | (h >> 1);
+        const uint32_t *sz = (const uint32_t *)(sl + WBYTES);
+        o.sc = f16_to_f32(sz[si]);
+        o.zs = -(f16_to_f32(sz[32 + si]) * o.sc);
+    };
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](const Ops &o) {
+        XV wfs[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const uint32_t p = (uint32_t)o.wv[t >> 2][t & 3];
+            const uint32_t lo = p & 0x0f0f0f0fu, hi = (p >> 4) & 0x0f0f0f0fu;   // even / odd k
+            float q0[4], q1[4];
+            ubytes_to_f32(lo, q0);
+            ubytes_to_f32(hi, q1);
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = pack2<XDT>(__builtin_fmaf(q0[e], o.sc, o.zs), __builtin_fmaf(q1[e], o.sc, o.zs));
+            wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            if constexpr (XDT == PSQ_BF16) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.xf[t], wfs[t], acc, 0, 0, 0);
+            else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.xf[t], wfs[t], acc, 0, 0, 0);
+        }
+    };
+    // Pipeline: block b + 1 is read while block b computes; block b's slot is refilled once its
+    // registers have been used (after compute).  Block b + 1 has landed when at most D - 2 younger
+    // blocks of this wave are in flight.
+    Ops oa, ob;
+    wait_vmcnt<LOADS * (D - 1)>();
+    read(0, 0, oa);
+    int slot = 0;
+    auto step = [&](int b, const Ops &cur, Ops &nxt) {
+        const int nslot = slot == D - 1 ? 0 : slot + 1;
+        wait_vmcnt<LOADS * (D - 2)>();
+        read(b + 1 < nb ? b + 1 : b, nslot, nxt);
+        compute(cur);
+        issue(b + D, slot);
+        slot = nslot;
+    };
+    for (int b = 0; b < nb; b += 2) {
+        step(b, oa, ob);
+        if (b + 1 < nb) step(b + 1, ob, oa);
+    }
+    wait_vmcnt<0>();
+    // y[m][n] = round_out(acc + bias[n]); lane: n = row0 + nr, m = 4 h + v
+    const int n = row0 + nr;
+    if (n < N) {
+        const float bb = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int m = 4 * h + v;
+            if (m < M) store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype, acc[v] + bb);
+        }
+    }
+}
+
+// The decode kernel's ring depth for M rows of K (0: the shape does not fit).
+int decode_depth(int64_t M, int64_t K)
+{
+    for (int d : {8, 6, 4})
+        if (wd::lds_bytes(M, K, d) <= 163840) return d;
+    return 0;
+}
+
+template <int XDT, int D>
+int launch_decode_d(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                    const char *name)
+{
+    auto kern = gemm_w4_decode<XDT, D>;
+    const int lds = (int)wd::lds_bytes(M, K, D);
+    if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
+        return set_error(PSQ_E_DEVICE, "%s: cannot reserve LDS", name);
+    const dim3 grid((unsigned)((N + wd::ROWS - 1) / wd::ROWS)), block(wd::NW * 64);
+    kern<<<grid, block, lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    return check_launch(name);
+}
+
+template <int XDT>
+int launch_decode(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                  const char *name)
+{
+    const int d = decode_depth(M, K);
+    if (d == 8) return launch_decode_d<XDT, 8>(x, ldx, M, N, K, wa, st, name);
+    if (d == 6) return launch_decode_d<XDT, 6>(x, ldx, M, N, K, wa, st, name);
+    return launch_decode_d<XDT, 4>(x, ldx, M, N, K, wa, st, name);
+}
+
 template <int XDT, int MT>
 int launch_stream_mt(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
                      const char *name)
@@ -897,10 +1071,13 @@ TiledPlan plan_tiled(int64_t M, int64_t N, int64_t K, int cus)
 // multiple of 128; the skinny kernel takes M <= SKINNY_MAX_M when K is a whole number of
 // 128-element blocks (and, for uint4, the groups hold whole 32-element lane runs); the tiled
 // kernel takes the rest.
-enum class Path { Stream, Skinny, Tiled };
+enum class Path { Decode, Stream, Skinny, Tiled };
 
 Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
 {
+    if (wk == W_UINT4 && M <= wd::MAXM && gs % 128 == 0 && K % 512 == 0 && decode_depth(M, K) > 0 &&
+        ldx <= (1LL << 22))
+        return Path::Decode;
     if (wk == W_UINT4 && PSQ_W4_STREAM && M <= SKINNY_MAX_M && gs % 128 == 0 &&
         K % (M <= 16 ? ws::BLK<1>() : ws::BLK<2>()) == 0 && ldx <= (1LL << 22))
         return Path::Stream;
@@ -924,6 +1101,9 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
 {
     const uint16_t *xp = (const uint16_t *)x;
     const Path path = choose_path(WK, ldx, M, K, wa.gs);
+    if (path == Path::Decode)
+        return x_dtype == PSQ_BF16 ? launch_decode<PSQ_BF16>(xp, ldx, M, N, K, wa, st, name)
+                                   : launch_decode<PSQ_F16>(xp, ldx, M, N, K, wa, st, name);
     if (path == Path::Stream)
         return x_dtype == PSQ_BF16 ? launch_stream<PSQ_BF16>(xp, ldx, M, N, K, wa, st, name)
                                    : launch_stream<PSQ_F16>(xp, ldx, M, N, K, wa, st, name);

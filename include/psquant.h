@@ -151,9 +151,10 @@ PSQ_API int psq_gemm_fp8_act(const uint8_t *a, int64_t lda, const float *a_scale
  * fp32 accumulation; y = round_out(acc + bias).  Replaces the int4 F.linear dispatch
  * (powershard/quant_linear.py:239, weight-only formats) and matches the dequantize
  * branch F.linear(rows, qt.dequantize().to(bf16), bias) (quant_linear.py:219-220).
- * The weight-streaming kernel (M <= 64, group_size a multiple of 128) and the tiled kernel
- * (M > 64) form w = round_bf16(fmaf(q, scale, -(zero * scale))), which differs from the formula
- * above by one bf16 ulp on about 2^-16 of the weights; both are within the fp32-accumulation bar.
+ * The decode kernel (M <= 4, group_size a multiple of 128, K a multiple of 512), the
+ * weight-streaming kernel (M <= 64, group_size a multiple of 128) and the tiled kernel (M > 64)
+ * form w = round_bf16(fmaf(q, scale, -(zero * scale))), which differs from the formula above by
+ * one bf16 ulp on about 2^-16 of the weights; all are within the fp32-accumulation bar.
  *   x [M, K] bf16 (ldx), wq [N, K/2] bytes (low nibble = even k), scale/zero [N, K/group]
  *   fp16, group_size a multiple of 64 dividing K. */
 PSQ_API int psq_gemm_w4a16(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq,

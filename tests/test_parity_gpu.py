@@ -346,3 +346,22 @@ def test_gemm_w4a16_unsplit_entry_point(gpu):
                             out_dtype=torch.float32)
     rms = ref.pow(2).mean().sqrt().item()
     assert (y.cpu() - ref).abs().max().item() <= 1e-2 * rms
+
+
+# ------------------------------------------------------------ W4A16 decode kernel (M <= 4)
+@pytest.mark.parametrize("M,N,K,gs", [(1, 25600, 5120, 128), (2, 2600, 5120, 128), (3, 389, 1024, 256),
+                                      (4, 1000, 3072, 128), (1, 130, 25600, 128), (4, 256, 512, 512)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_gemm_w4a16_decode(gpu, M, N, K, gs, xdt):
+    """M <= 4 with K % 512 == 0 runs the barrier-free decode kernel (activations in LDS, a private
+    weight ring per wave); same bar as the other weight-only paths."""
+    from powershard_amd import ops
+    x = heavy_rows(M, K, seed=110 + M, outlier_frac=0, dtype=xdt)
+    w = torch.randn(N, K, generator=seeded(111)) * 0.02
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    b = (torch.randn(N, generator=seeded(112)) * 0.01).to(xdt)
+    args = (x.to(gpu), wq.to(gpu), s.to(gpu), z.to(gpu), gs, b.to(gpu))
+    y32 = ops.gemm_w4a16(*args, out_dtype=torch.float32)
+    yb = ops.gemm_w4a16(*args, out_dtype=torch.bfloat16)
+    wd = oracle.dequant_uint4(wq, s, z, gs, out_dtype=xdt)
+    assert_fp32_path(y32, yb, oracle.gemm_wonly(x, wd, None, b, out_dtype=torch.float32), f"w4a16 decode {M}x{N}x{K}")
