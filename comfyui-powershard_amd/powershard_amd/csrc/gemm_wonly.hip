@@ -198,29 +198,36 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
 }
 
 // ------------------------------------------------------------------ tiled kernel (M > 64)
-// A BM x 256 output tile (BM = 256, or 128 when that fills more of the GPU) per workgroup of 4
-// waves.  Wave w owns all BM rows (tokens) and the 64 weight rows (output columns) 64w .. 64w + 63:
-// BM/32 x 2 MFMA tiles of 32 x 32 on v_mfma_f32_32x32x16_bf16 / f16 with the accumulators in
-// AGPRs.  So every weight element is dequantized once per workgroup, by the one wave that
-// multiplies it, for BM rows.  K runs in
+// A BM x 256 output tile (BM = 256, or 128 when that fills more of the GPU) per workgroup of 8
+// waves, two per SIMD.  Wave w owns all BM rows (tokens) and the 32 weight rows (output columns)
+// 32w .. 32w + 31: BM/32 MFMA tiles of 32 x 32 on v_mfma_f32_32x32x16_bf16 / f16 with the
+// accumulators in AGPRs.  So every weight element is dequantized once per workgroup, by the one
+// wave that multiplies it, for BM rows.  Two waves per SIMD because the dequantization is VALU
+// work that one wave cannot issue fast enough beside its own MFMAs: on gfx950 a single wave issues
+// a v_fma_f32 every ~5.3 cycles and a v_cvt_f32_ubyte / v_cvt_pk_bf16_f32 every 8, two waves of a
+// SIMD together one every ~3.3 / ~4.5, and the other wave's MFMAs run meanwhile.  K runs in
 // stages of 64 through a 3-deep LDS ring filled by global->LDS loads: per stage the activations
 // (BM rows x 128 bytes, XOR-swizzled 16-byte chunks), the packed weights (256 rows x 32 bytes of
 // nibbles, or 64 bytes of int8) and, for uint4, each weight row's group scale and zero (one
-// 32-bit word each, zero-extended fp16).  Inside a stage the MFMAs of k-step t run beside the
+// 32-bit word each, zero-extended fp16; waves 0-3 load the scales of 64 columns each, waves 4-7
+// the zeros).  Inside a stage the MFMAs of k-step t run beside the
 // activation fragment reads and the weight dequantization of k-step t + 1; the stage's one
 // barrier sits before its last k-step, whose MFMAs cover the next stage's first reads and
 // dequantization.  Lane-half h of every fragment carries k = 32 h + 8 t .. + 7 of the stage in
 // k-step t, for both operands, so a lane's weights of a stage are 16 contiguous bytes of nibbles.
 namespace wt {
 constexpr int BN = 256, BK = 64;
-constexpr int TN = 2;                              // 32 x 32 tiles per wave: BM rows x 64 columns
+constexpr int TN = 1;                              // 32 x 32 tiles per wave: BM rows x 32 columns
+constexpr int WCOLS = 32 * TN;                     // output columns per wave
+constexpr int NWAVE = BN / WCOLS;                  // waves per workgroup (8: two per SIMD)
+constexpr int THREADS = NWAVE * 64;
 constexpr int XROW = BK * 2;                       // activation bytes per row per stage
 template <int BM> constexpr int xbytes() { return BM * XROW; }                        // 32 / 16 KB
-template <int BM> constexpr int xdma() { return xbytes<BM>() / 1024 / 4; }            // activation loads per wave (8 / 4)
+template <int BM> constexpr int xdma() { return xbytes<BM>() / 1024 / NWAVE; }        // activation loads per wave (4 / 2)
 template <int WK> constexpr int wrow() { return WK == W_UINT4 ? BK / 2 : BK; }         // 32 / 64 B
-template <int WK> constexpr int wdma() { return BN * wrow<WK>() / 1024 / 4; }          // 2 / 4
-template <int WK> constexpr int szdma() { return WK == W_UINT4 ? 2 : 0; }
-template <int WK, int BM> constexpr int lps() { return xdma<BM>() + wdma<WK>() + szdma<WK>(); }   // 12 / 12 (BM 256)
+template <int WK> constexpr int wdma() { return BN * wrow<WK>() / 1024 / NWAVE; }      // 1 / 2
+template <int WK> constexpr int szdma() { return WK == W_UINT4 ? 1 : 0; }
+template <int WK, int BM> constexpr int lps() { return xdma<BM>() + wdma<WK>() + szdma<WK>(); }   // 6 / 6 (BM 256)
 template <int WK, int BM> constexpr int slot_bytes() { return xbytes<BM>() + BN * wrow<WK>() + (WK == W_UINT4 ? 2 * BN * 4 : 0); }
 #ifndef PSQ_WT_NS128
 #define PSQ_WT_NS128 3
@@ -230,14 +237,21 @@ template <int WK, int BM> constexpr int nstage()
 {
     return BM == 256 ? 3 : (163840 / slot_bytes<WK, BM>() < PSQ_WT_NS128 ? 163840 / slot_bytes<WK, BM>() : PSQ_WT_NS128);
 }
-template <int WK, int BM> constexpr int lds_bytes() { return nstage<WK, BM>() * slot_bytes<WK, BM>(); }   // 126 / 144 KB (BM 256)
+// uint4 group scales and zeros in blocks of SZG groups: per block and column 16 bytes of scales and
+// 16 of zeros (one dense 16-byte load per lane), two blocks buffered past the ring
+constexpr int SZG = 8;
+constexpr int SZB_BYTES = 2 * BN * 16;
+template <int WK, int BM> constexpr int lds_bytes()
+{
+    return nstage<WK, BM>() * slot_bytes<WK, BM>() + (WK == W_UINT4 ? 2 * SZB_BYTES : 0);   // 142 KB (uint4, BM 256)
+}
 // activation chunk swizzle: bijective on 8 consecutive rows (32 banks) and on each parity class
 // of 16 consecutive rows (64 banks), so a fragment read (32 rows, one logical chunk) is conflict free
 __device__ __forceinline__ int xsw(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
 }  // namespace wt
 
 template <int XDT, int WK, int BM>
-__global__ void __launch_bounds__(NTHREADS, 1)
+__global__ void __launch_bounds__(wt::THREADS, 1)
 gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
 {
     using namespace wt;
@@ -271,19 +285,26 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     uint32_t xo[XDMA], wo[WDMA];
 #pragma unroll
     for (int j = 0; j < XDMA; j++) {
-        const int b = j * 4 + wave, r = 8 * b + (lane >> 3);
+        const int b = j * NWAVE + wave, r = 8 * b + (lane >> 3);
         const int c = (lane & 7) ^ xsw(r);
         xo[j] = (uint32_t)(min(r, M - 1 - m0) * ldx * 2 + c * 16);
     }
 #pragma unroll
     for (int j = 0; j < WDMA; j++) {
-        const int b = j * 4 + wave;
+        const int b = j * NWAVE + wave;
         const int per = 1024 / RB;                          // rows per load (32 / 16)
         const int r = per * b + lane / (64 / per);
         wo[j] = (uint32_t)(min(r, N - 1 - n0) * wld + (lane % (64 / per)) * 16);
     }
-    const int scol = min(n0 + 64 * wave + lane, N - 1);      // scale / zero column of this lane
+    const int scol = min(n0 + 64 * (wave & 3) + lane, N - 1);   // scale (waves 0-3) / zero (4-7) column of this lane
     const unsigned spg = WK == W_UINT4 ? (unsigned)(wa.gs / BK) : 1u;   // stages per group
+    // Scale / zero blocks (uint4, groups per row a multiple of SZG, 16-byte aligned tables): a
+    // block of SZG groups is loaded once, with the first stage of the block (or of the workgroup's
+    // K range), instead of a 2-byte scattered load per stage.  Otherwise the per-stage loads.
+    const bool szblk = WK == W_UINT4 && G % SZG == 0 && ((uintptr_t)wa.scale16 % 16) == 0 &&
+                       ((uintptr_t)wa.zero16 % 16) == 0;
+    const unsigned spb = spg * SZG;                           // stages per scale block
+    uint8_t *const szbuf = smem + NSTAGE * SLOT;
     const uint8_t *xb = (const uint8_t *)(x + (int64_t)m0 * ldx);
     const uint8_t *wb = wa.wq + (int64_t)n0 * wld;
     // The tile's activation and weight rows as buffer descriptors: a load is the descriptor, the
@@ -296,17 +317,26 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         constexpr int q = decltype(qc)::value;
         uint8_t *sl = smem + slot * SLOT;
         if constexpr (q < XDMA) {
-            constexpr int b4 = q * 4;
-            buffer_load_lds16(rsx, (lds_ptr)(sl + 1024 * (b4 + wave)), xo[q], kt * BK * 2);
+            constexpr int b8 = q * NWAVE;
+            buffer_load_lds16(rsx, (lds_ptr)(sl + 1024 * (b8 + wave)), xo[q], kt * BK * 2);
         } else if constexpr (q < XDMA + WDMA) {
             constexpr int j = q - XDMA;
-            buffer_load_lds16(rsw, (lds_ptr)(sl + XBYTES + 1024 * (j * 4 + wave)), wo[j], kt * RB);
+            buffer_load_lds16(rsw, (lds_ptr)(sl + XBYTES + 1024 * (j * NWAVE + wave)), wo[j], kt * RB);
         } else if constexpr (WK == W_UINT4) {
-            constexpr bool zero = q == LPS - 1;
-            const int64_t gi = (int64_t)scol * G + (int)((unsigned)kt / spg);   // the stage's group
-            __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
-                                             (lds_ptr)(sl + XBYTES + BN * RB + (zero ? BN * 4 : 0) + 256 * wave), 2, 0,
-                                             0);
+            const bool zero = wave >= 4;
+            if (szblk) {
+                // the block of the stage's group, with the block's first stage (or the range's)
+                if (kt == kb || (unsigned)kt % spb == 0) {
+                    const unsigned blk = (unsigned)kt / spb;
+                    const int64_t gi = (int64_t)scol * G + SZG * blk;
+                    __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
+                                                     (lds_ptr)(szbuf + (blk & 1) * SZB_BYTES + 1024 * wave), 16, 0, 0);
+                }
+            } else {
+                const int64_t gi = (int64_t)scol * G + (int)((unsigned)kt / spg);   // the stage's group
+                __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
+                                                 (lds_ptr)(sl + XBYTES + BN * RB + 256 * wave), 2, 0, 0);
+            }
         }
     };
     auto issue_all = [&](int slot, int kt) {
@@ -324,16 +354,23 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     // the columns' group scale s and -z s: a weight is round_16(fmaf(q, s, -z s)), one VALU op
     // (as in the streaming kernel)
     struct WRaw { v4i w[TN][RB / 32]; float s[TN], z[TN]; };
-    auto read_w = [&](int slot, WRaw &r) {
+    auto read_w = [&](int slot, int kt, WRaw &r) {
         const uint8_t *sl = smem + slot * SLOT + XBYTES;
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int n = 64 * wave + 32 * j + frow;
+            const int n = WCOLS * wave + 32 * j + frow;
 #pragma unroll
             for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
             if constexpr (WK == W_UINT4) {
-                r.s[j] = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
-                r.z[j] = -(f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n)) * r.s[j]);   // -z s
+                if (szblk) {
+                    const unsigned g = (unsigned)kt / spg;
+                    const uint8_t *zb = szbuf + ((g / SZG) & 1) * SZB_BYTES + 16 * n + 2 * (g % SZG);
+                    r.s[j] = f16_to_f32(*(const uint16_t *)zb);
+                    r.z[j] = -(f16_to_f32(*(const uint16_t *)(zb + BN * 16)) * r.s[j]);   // -z s
+                } else {
+                    r.s[j] = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
+                    r.z[j] = -(f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n)) * r.s[j]);   // -z s
+                }
             } else {
                 r.s[j] = 1.0f;
                 r.z[j] = 0.0f;
@@ -369,13 +406,26 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, xf, acc[i][j], 0, 0, 0);
     };
 
+    // Stage kt + 1 landed: every load but those of the NSTAGE - 2 younger stages is complete.  With
+    // scale blocks a stage issues LPS - 1 loads plus, at a block start, the block's: counting only
+    // the LPS - 1 waits for at least the loads it must (the block's is older than the younger
+    // stages' loads).
+    auto wait_stage = [&] {
+        if constexpr (WK == W_UINT4) {
+            if (szblk) wait_vmcnt<(NSTAGE - 2) * (LPS - 1)>();
+            else wait_vmcnt<(NSTAGE - 2) * LPS>();
+        } else {
+            wait_vmcnt<(NSTAGE - 2) * LPS>();
+        }
+    };
+
     // ---- prologue: stages 0 .. NSTAGE-2 in flight, stage 0 landed, its first fragments ready
 #pragma unroll
     for (int st = 0; st < NSTAGE - 1; st++) issue_all(st, kb + min(st, nk - 1));
-    wait_vmcnt<(NSTAGE - 2) * LPS>();
+    wait_stage();
     stage_barrier();
     WRaw wr;
-    read_w(0, wr);
+    read_w(0, kb, wr);
     XV xa[TM], xb2[TM], wa0[TN], wb0[TN];
 #pragma unroll
     for (int i = 0; i < TM; i++) xa[i] = read_x(0, 0, i);
@@ -387,9 +437,9 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         wa0[j] = __builtin_bit_cast(XV, v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]});
     }
 
-    // One k-step: the 16 MFMAs of step t on (xc, wc); behind MFMA q the activation fragment
-    // q / 2 of the next step (even q), a weight pair of the next step (odd q: column tile
-    // q / 8, pair (q / 2) % 4), and for k-steps 0-2 a third of the stage's refill loads (q % 4 == 3).
+    // One k-step: the NQ = TM TN MFMAs of step t on (xc, wc); behind MFMA q the activation
+    // fragment q / TN of the next step (q % TN == 0), one of the next step's 4 TN weight pairs
+    // (every NQ / (4 TN)-th MFMA), and for k-steps 0-2 a third of the stage's refill loads.
     // The instruction order is pinned: sched_barrier after every MFMA.
     auto kstep = [&](auto tnc, auto basec, XV (&xc)[TM], XV (&wc)[TN], XV (&xn)[TM], XV (&wn)[TN], int xslot,
                      const WRaw &wraw, int fill_slot, int fill_kt) {
@@ -398,12 +448,12 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         [&]<int... Q>(std::integer_sequence<int, Q...>) {
             ([&] {
                 constexpr int q = Q;
-                mfma(q >> 1, q & 1, wc[q & 1], xc[q >> 1]);
-                if constexpr ((q & 1) == 0) xn[q >> 1] = read_x(xslot, tn, q >> 1);
-                // weight pair pi (column tile pi / 4, pair pi % 4): behind the odd MFMAs of a
-                // 16-MFMA k-step, behind every MFMA of an 8-MFMA one (7 VALU ops a pair, one MFMA's
-                // worth of issue slots)
-                constexpr int pi = NQ >= 16 ? ((q & 1) ? (q >> 1) : -1) : q;
+                mfma(q / TN, q % TN, wc[q % TN], xc[q / TN]);
+                if constexpr (q % TN == 0) xn[q / TN] = read_x(xslot, tn, q / TN);
+                // weight pair pi (column tile pi / 4, pair pi % 4), spread evenly over the k-step
+                constexpr int NP = 4 * TN, PSTRIDE = NQ / NP;
+                static_assert(NQ % NP == 0, "pairs per k-step must divide the MFMAs");
+                constexpr int pi = q % PSTRIDE == 0 ? q / PSTRIDE : -1;
                 if constexpr (pi >= 0) hw[pi >> 2][pi & 3] = dq_pair(wraw, pi >> 2, tn, pi & 3);
                 // the refill loads: LPK of them spread over the k-step, the last of each group
                 constexpr int per = NQ / LPK, u = q / per;
@@ -426,9 +476,9 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         kstep(std::integral_constant<int, 2>{}, std::integral_constant<int, LPK>{}, xb2, wb0, xa, wa0, rs, wr, fill, kfill);
         kstep(std::integral_constant<int, 3>{}, std::integral_constant<int, 2 * LPK>{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
         // stage kt + 1 landed for every wave; nobody reads stage kt's slot any more
-        wait_vmcnt<(NSTAGE - 2) * LPS>();
+        wait_stage();
         stage_barrier();
-        read_w(nxt, wr);
+        read_w(nxt, kb + kt + 1, wr);
         kstep(I{}, std::integral_constant<int, -1>{}, xb2, wb0, xa, wa0, nxt, wr, 0, 0);
         rs = nxt;
     }
@@ -443,8 +493,8 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
                 constexpr int j = decltype(jc)::value;
                 static_for<4>([&](auto gc) {
                     constexpr int g = decltype(gc)::value;
-                    // lane (row 32 i + frow) holds columns 64 wave + 32 j + 8 g + 4 h + 0..3
-                    float *o = part + (32 * i + frow) * BN + 64 * wave + 32 * j + 8 * g + 4 * h;
+                    // lane (row 32 i + frow) holds columns WCOLS wave + 32 j + 8 g + 4 h + 0..3
+                    float *o = part + (32 * i + frow) * BN + WCOLS * wave + 32 * j + 8 * g + 4 * h;
                     *(v4f *)o = v4f{__int_as_float(agpr_read(acc[i][j][4 * g])),
                                     __int_as_float(agpr_read(acc[i][j][4 * g + 1])),
                                     __int_as_float(agpr_read(acc[i][j][4 * g + 2])),
@@ -456,9 +506,9 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     }
 
     // ---- epilogue: acc[i][j] is the transposed 32 x 32 tile, lane (l & 31) holds output row
-    // m = m0 + 32 i + (l & 31), register 4g + c column n = n0 + 64 wave + 32 j + 8 g + 4 h + c.
+    // m = m0 + 32 i + (l & 31), register 4g + c column n = n0 + WCOLS wave + 32 j + 8 g + 4 h + c.
     //   y = round_out(fmaf(acc, s[n], bias[n]))   (s = 1 for uint4)
-    const int nl0 = 64 * wave + 4 * h;                       // the lane's first column in the tile
+    const int nl0 = WCOLS * wave + 4 * h;                    // the lane's first column in the tile
     const int esz = wa.y_dtype == PSQ_F32 ? 4 : 2;
     uint8_t *rowp[TM];
     bool live[TM];
@@ -1012,7 +1062,7 @@ int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_
         attr_set[dev] = true;
     }
     const int64_t tiles = ((M + BM - 1) / BM) * ((N + wt::BN - 1) / wt::BN);
-    kern<<<dim3((unsigned)(tiles * wa.ksplit)), dim3(NTHREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    kern<<<dim3((unsigned)(tiles * wa.ksplit)), dim3(wt::THREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
     if (wa.ksplit > 1) {
         if (int e = check_launch(name)) return e;
         const int64_t threads = M * ((N + 3) / 4);
