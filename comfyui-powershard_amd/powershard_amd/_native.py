@@ -32,6 +32,7 @@ SIGNATURES = {
     "psq_gemm_i8_act": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_i8_i32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_fp8": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
+    "psq_gemm_fp8_e5m2w": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_fp8_act": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_w4a16": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_w8a16": (_I, [_P, _I, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
@@ -42,6 +43,7 @@ SIGNATURES = {
     "psq_dequant_uint4": (_I, [_P, _P, _P, _I, _I64, _I64, _P, _I, _P]),
     "psq_dequant_i8_rows": (_I, [_P, _P, _I64, _I64, _I, _P, _I, _P]),
     "psq_dequant_fp8": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _P]),
+    "psq_dequant_e5m2": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _P]),
 }
 
 

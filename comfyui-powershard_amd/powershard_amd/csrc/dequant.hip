@@ -53,7 +53,8 @@ dequant_uint4_kernel(const uint8_t *__restrict__ wq, const uint16_t *__restrict_
     store16<ODT>(out, n * K + k0, v);
 }
 
-template <int ODT>
+// fp8 weights: E5M2 false decodes e4m3fn codes, true e5m2 codes
+template <int ODT, bool E5M2>
 __global__ void __launch_bounds__(NT)
 dequant_fp8_kernel(const uint8_t *__restrict__ q, const float *__restrict__ sc, int per_row, int64_t N, int64_t K,
                    void *__restrict__ out)
@@ -66,7 +67,10 @@ dequant_fp8_kernel(const uint8_t *__restrict__ q, const float *__restrict__ sc, 
     const float s = sc[per_row ? n : 0];
     float v[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = e4m3_to_f32(((uint32_t)p[i >> 2] >> (8 * (i & 3))) & 0xffu) * s;
+    for (int i = 0; i < 16; i++) {
+        const uint32_t c = ((uint32_t)p[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        v[i] = (E5M2 ? e5m2_to_f32(c) : e4m3_to_f32(c)) * s;
+    }
     store16<ODT>(out, n * K + k0, v);
 }
 
@@ -132,6 +136,24 @@ int check_out(const char *name, int64_t N, int64_t K, const void *out, int out_d
 
 unsigned blocks_for(int64_t n) { return (unsigned)((n + NT - 1) / NT); }
 
+template <bool E5M2>
+int dequant_fp8_any(const uint8_t *q, const float *w_scale, int w_scale_per_row, int64_t N, int64_t K, void *out,
+                    int out_dtype, void *stream, const char *name)
+{
+    if (int e = check_out(name, N, K, out, out_dtype)) return e;
+    if (N == 0 || K == 0) return PSQ_OK;
+    if (!q || !w_scale) return set_error(PSQ_E_ARG, "%s: null pointer", name);
+    if ((uintptr_t)q & 15) return set_error(PSQ_E_SHAPE, "%s: weights must be 16-byte aligned", name);
+    if (int e = require_device()) return e;
+    const unsigned nb = blocks_for(N * (K / 16));
+    hipStream_t st = (hipStream_t)stream;
+    const int pr = w_scale_per_row ? 1 : 0;
+    if (out_dtype == PSQ_BF16) dequant_fp8_kernel<PSQ_BF16, E5M2><<<nb, NT, 0, st>>>(q, w_scale, pr, N, K, out);
+    else if (out_dtype == PSQ_F16) dequant_fp8_kernel<PSQ_F16, E5M2><<<nb, NT, 0, st>>>(q, w_scale, pr, N, K, out);
+    else dequant_fp8_kernel<PSQ_F32, E5M2><<<nb, NT, 0, st>>>(q, w_scale, pr, N, K, out);
+    return check_launch(name);
+}
+
 }  // namespace
 }  // namespace psq
 
@@ -160,19 +182,13 @@ int psq_dequant_uint4(const uint8_t *wq, const uint16_t *w_scale, const uint16_t
 int psq_dequant_fp8(const uint8_t *q, const float *w_scale, int w_scale_per_row, int64_t N, int64_t K, void *out,
                     int out_dtype, void *stream)
 {
-    using namespace psq;
-    if (int e = check_out("dequant_fp8", N, K, out, out_dtype)) return e;
-    if (N == 0 || K == 0) return PSQ_OK;
-    if (!q || !w_scale) return set_error(PSQ_E_ARG, "dequant_fp8: null pointer");
-    if ((uintptr_t)q & 15) return set_error(PSQ_E_SHAPE, "dequant_fp8: weights must be 16-byte aligned");
-    if (int e = require_device()) return e;
-    const unsigned nb = blocks_for(N * (K / 16));
-    hipStream_t st = (hipStream_t)stream;
-    const int pr = w_scale_per_row ? 1 : 0;
-    if (out_dtype == PSQ_BF16) dequant_fp8_kernel<PSQ_BF16><<<nb, NT, 0, st>>>(q, w_scale, pr, N, K, out);
-    else if (out_dtype == PSQ_F16) dequant_fp8_kernel<PSQ_F16><<<nb, NT, 0, st>>>(q, w_scale, pr, N, K, out);
-    else dequant_fp8_kernel<PSQ_F32><<<nb, NT, 0, st>>>(q, w_scale, pr, N, K, out);
-    return check_launch("dequant_fp8");
+    return psq::dequant_fp8_any<false>(q, w_scale, w_scale_per_row, N, K, out, out_dtype, stream, "dequant_fp8");
+}
+
+int psq_dequant_e5m2(const uint8_t *q, const float *w_scale, int w_scale_per_row, int64_t N, int64_t K, void *out,
+                     int out_dtype, void *stream)
+{
+    return psq::dequant_fp8_any<true>(q, w_scale, w_scale_per_row, N, K, out, out_dtype, stream, "dequant_e5m2");
 }
 
 int psq_dequant_i8_rows(const int8_t *q, const float *w_scale, int64_t N, int64_t K, int rot_group, void *out,

@@ -4,7 +4,8 @@
 // F.linear(QuantizedTensor, QuantizedTensor, bias) (powershard/quant_linear.py:230-242).
 //   y[m][n] = round_out(fmaf((float)acc[m][n], a_scale[m] * w_scale[n], bias[n]))
 //   int8: acc = sum_k a[m][k] w[n][k] in int32 (v_mfma_i32_32x32x32_i8, exact)
-//   fp8 : acc = the same in fp32 (v_mfma_f32_32x32x64_f8f6f4, e4m3 x e4m3)
+//   fp8 : acc = the same in fp32 (v_mfma_f32_32x32x64_f8f6f4, e4m3 x e4m3; or e5m2 weights x
+//         e4m3 activations, the instruction's A-operand format selector set to bf8)
 // With an epilogue activation (GELU, tanh form; the Wan FFN's F.gelu(fc1(x).float(),
 // approximate="tanh"), powershard/wan_model.py:626) the store writes round_out(act(round_out(y))):
 // the GELU of the rounded linear output, rounded to the dtype the next layer casts it to.
@@ -254,7 +255,8 @@ __device__ __forceinline__ float bias_word(uint32_t w, int dt)
 // epilogue runs.  The MFMAs compute the transposed tile (W fragment as the first operand), which
 // gives each lane one output row and, per 32 x 32 tile, four runs of 4 consecutive columns: the
 // epilogue converts the accumulators in registers and stores them directly.
-template <bool FP8, int OUT, int ACT>
+// WF: the fp8 weights' format (0: e4m3fn, 1: e5m2), the f8f6f4 MFMA's A-operand format code.
+template <bool FP8, int OUT, int ACT, int WF = 0>
 __global__ void __launch_bounds__(NTHREADS, 1)
 gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W, int64_t ldw,
                int M, int N, int K, Epi ep)
@@ -420,7 +422,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     Acc acc[TM][TN];
     auto mfma = [&](int i, int j, const FT (&fa)[TM], const FT (&fw)[TN]) {
         if constexpr (FP8)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], acc[i][j], WF, 0, 0, 127, 0, 127);
         else
             acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
     };
@@ -958,11 +960,11 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     wait_vmcnt<0>();
 }
 
-template <bool FP8, int OUT, int ACT>
+template <bool FP8, int OUT, int ACT, int WF = 0>
 int launch_one(const uint8_t *a, int64_t lda, const uint8_t *w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                const Epi &ep, hipStream_t st, const char *name)
 {
-    auto kern = gemm_q8_kernel<FP8, OUT, ACT>;
+    auto kern = gemm_q8_kernel<FP8, OUT, ACT, WF>;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
     static bool attr_set[64] = {};   // per device; the attribute is idempotent
@@ -1114,6 +1116,28 @@ int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, const uint
 {
     return psq_gemm_fp8_act(a, lda, a_scale, w, ldw, w_scale, w_scale_per_row, bias, bias_dtype, PSQ_ACT_NONE, y,
                             y_dtype, ldy, M, N, K, stream);
+}
+
+int psq_gemm_fp8_e5m2w(const uint8_t *a, int64_t lda, const float *a_scale, const uint8_t *w, int64_t ldw,
+                       const float *w_scale, int w_scale_per_row, const void *bias, int bias_dtype, void *y,
+                       int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream)
+{
+    using namespace psq;
+    if (int e = check_shapes("gemm_fp8_e5m2w", a, lda, w, ldw, M, N, K)) return e;
+    if (int e = check_act("gemm_fp8_e5m2w", PSQ_ACT_NONE, N, ldw, K, ldy)) return e;
+    if (M == 0 || N == 0) return PSQ_OK;
+    if (!a_scale || !w_scale || !y) return set_error(PSQ_E_ARG, "gemm_fp8_e5m2w: null scale or output");
+    if (!valid_dtype(y_dtype) || (bias && !valid_dtype(bias_dtype)))
+        return set_error(PSQ_E_ARG, "gemm_fp8_e5m2w: bad dtype");
+    if (int e = require_device()) return e;
+    Epi ep{a_scale, w_scale, w_scale_per_row ? 1 : 0, bias, bias_dtype, y, ldy, vec_ok(y, ldy, y_dtype == PSQ_F32 ? 4 : 2)};
+    hipStream_t st = (hipStream_t)stream;
+    const char *name = "gemm_fp8_e5m2w";
+    switch (y_dtype) {
+    case OUT_BF16: return launch_one<true, OUT_BF16, ACT_NONE, 1>(a, lda, w, ldw, M, N, K, ep, st, name);
+    case OUT_F16: return launch_one<true, OUT_F16, ACT_NONE, 1>(a, lda, w, ldw, M, N, K, ep, st, name);
+    default: return launch_one<true, OUT_F32, ACT_NONE, 1>(a, lda, w, ldw, M, N, K, ep, st, name);
+    }
 }
 
 }  // extern "C"

@@ -111,6 +111,14 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c)
     return (c & 0x80u) ? -v : v;
 }
 
+// OCP e5m2 (bf8) code to fp32: the code is the high byte of the fp16 with the same value (1 sign,
+// 5 exponent bits of bias 15, 2 mantissa bits; subnormals, infinities and NaNs included), so the
+// decode is exact.
+__device__ __forceinline__ float e5m2_to_f32(uint32_t c)
+{
+    return f16_to_f32((c & 0xffu) << 8);
+}
+
 // ------------------------------------------------------------------ activations
 // GELU, tanh approximation: gelu(x) = x (1 + tanh z) / 2 with z = sqrt(2/pi) (x + 0.044715 x^3).
 // (1 + tanh z) / 2 is the logistic function of 2 z, so gelu(x) = x / (1 + 2^(x (k0 + k1 x^2)))

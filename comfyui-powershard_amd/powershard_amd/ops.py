@@ -194,15 +194,20 @@ def gemm_i8_i32(a, w):
 
 
 def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activation=None):
-    """fp8 e4m3fn GEMM: y = round(fmaf(a @ w.T (fp32), a_scale[m] * w_scale[n or 0], bias[n])).
+    """fp8 GEMM: y = round(fmaf(a @ w.T (fp32), a_scale[m] * w_scale[n or 0], bias[n])).
 
-    activation as in gemm_i8.
+    a: e4m3fn activation codes.  w: e4m3fn codes, or float8_e5m2 codes (``psq_gemm_fp8_e5m2w``,
+    no activation epilogue).  uint8 views are read as e4m3fn.  activation as in gemm_i8.
     """
     _need_gpu(a, a_scale, w, w_scale)
     a, w = _rows2d(a), _rows2d(w)
-    for t in (a, w):
-        if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
-            raise TypeError("gemm_fp8: operands must be float8_e4m3fn")
+    if a.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise TypeError("gemm_fp8: activations must be float8_e4m3fn")
+    e5m2 = w.dtype == torch.float8_e5m2
+    if w.dtype not in (torch.float8_e4m3fn, torch.uint8) and not e5m2:
+        raise TypeError("gemm_fp8: weights must be float8_e4m3fn or float8_e5m2")
+    if e5m2 and activation not in (None, "none"):
+        raise ValueError("gemm_fp8: float8_e5m2 weights take no activation epilogue")
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K:
@@ -219,7 +224,8 @@ def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activa
                 _p(w_scale), int(w_scale.numel() > 1), _p(bias), bdt, act, _p(y), _dt(y, "out"), y.shape[1], M, N, K,
                 _stream(a))
     else:
-        _launch("gemm_fp8", _native.lib().psq_gemm_fp8, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0),
+        fn = _native.lib().psq_gemm_fp8_e5m2w if e5m2 else _native.lib().psq_gemm_fp8
+        _launch("gemm_fp8", fn, _p(a), a.stride(0), _p(a_scale), _p(w), w.stride(0),
                 _p(w_scale), int(w_scale.numel() > 1), _p(bias), bdt, _p(y), _dt(y, "out"), N, M, N, K, _stream(a))
     return y
 
@@ -304,14 +310,18 @@ def dequant_i8_rows(q, w_scale, rot_group=0, out_dtype=torch.bfloat16):
     return out
 
 
-def dequant_fp8(q, w_scale, out_dtype=torch.bfloat16):
+def dequant_fp8(q, w_scale, out_dtype=torch.bfloat16, e5m2=None):
+    """fp8 weight codes [N, K] times the scale (one, or one per row).  e5m2: the codes are
+    float8_e5m2 (default: from q's dtype; uint8 views are e4m3fn)."""
     _need_gpu(q)
+    if e5m2 is None:
+        e5m2 = q.dtype == torch.float8_e5m2
     q = q.contiguous()
     N, K = q.shape
     s = w_scale.to(device=q.device, dtype=torch.float32).reshape(-1).contiguous()
     out = torch.empty(N, K, dtype=out_dtype, device=q.device)
-    _launch("dequant_fp8", _native.lib().psq_dequant_fp8, _p(q), _p(s), int(s.numel() > 1), N, K, _p(out), _dt(out, "out"),
-                                                _stream(q))
+    name, fn = ("dequant_e5m2", _native.lib().psq_dequant_e5m2) if e5m2 else ("dequant_fp8", _native.lib().psq_dequant_fp8)
+    _launch(name, fn, _p(q), _p(s), int(s.numel() > 1), N, K, _p(out), _dt(out, "out"), _stream(q))
     return out
 
 

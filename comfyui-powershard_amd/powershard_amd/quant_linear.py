@@ -44,7 +44,8 @@ ALIGN = 16
 # input_scale is a static activation scale.  Stored in the same byte vector as "x:<name>".
 EXTRAS = ("pre_quant_scale", "input_scale")
 # Formats with a native kernel here and the library op that runs them.
-NATIVE = {"int8_tensorwise": "gemm_i8", "float8_e4m3fn": "gemm_fp8", "int4_asym_group": "gemm_w4a16"}
+NATIVE = {"int8_tensorwise": "gemm_i8", "float8_e4m3fn": "gemm_fp8", "float8_e5m2": "gemm_fp8",
+          "int4_asym_group": "gemm_w4a16"}
 # The exceptions of a native attempt that switch a module to dequantize (quant_linear.py:207-215).
 NATIVE_FAILURES = (NotImplementedError, RuntimeError, TypeError, ValueError)
 
@@ -177,8 +178,8 @@ def quantized_from_file(handle, entries, module, conf, shape, device, dtype, met
     entries: name -> file key (or, with meta=True, name -> (torch dtype, shape): a template
     without reading data).  conf: the module's ``comfy_quant`` JSON.  Layouts on disk:
     int8_tensorwise = weight I8 [N, K] + weight_scale F32 [N, 1] (+ convrot,
-    convrot_groupsize); float8_e4m3fn = weight F8_E4M3 + weight_scale / scale_weight F32 ([] or
-    [N]); int4_asym_group = weight U8 [N, K/2] + weight_scale / weight_zero F16 [N, K/g] (+ group_size).
+    convrot_groupsize); float8_e4m3fn / float8_e5m2 = weight F8_E4M3 / F8_E5M2 + weight_scale /
+    scale_weight F32 ([] or [N]); int4_asym_group = weight U8 [N, K/2] + weight_scale / weight_zero F16 [N, K/g] (+ group_size).
     """
     prefix = module + "."
     fmt = conf.get("format")
@@ -199,10 +200,12 @@ def quantized_from_file(handle, entries, module, conf, shape, device, dtype, met
         params = qtm.Int8RowwiseParams(scale.to(dev, torch.float32).reshape(n, 1), dtype, rot["convrot"],
                                        rot["group_size"])
         return qtm.QuantizedWeight(weight.to(dev), qtm.Int8RowwiseLayout, params)
-    if fmt == "float8_e4m3fn":
+    if fmt in ("float8_e4m3fn", "float8_e5m2"):
+        code = torch.float8_e4m3fn if fmt == "float8_e4m3fn" else torch.float8_e5m2
         scale = state.get(prefix + "weight_scale", state.get(prefix + "scale_weight"))
-        if weight.dtype != torch.float8_e4m3fn or scale is None:
-            raise ValueError(f"{module}: float8_e4m3fn expects F8_E4M3 weight and a weight_scale")
+        if weight.dtype != code or scale is None:
+            raise ValueError(f"{module}: {fmt} expects {'F8_E4M3' if fmt == 'float8_e4m3fn' else 'F8_E5M2'} "
+                             "weight and a weight_scale")
         scale = scale.to(dev, torch.float32)
         scale = scale.reshape(()) if scale.numel() == 1 else scale.reshape(n)
         return qtm.QuantizedWeight(weight.to(dev), qtm.Float8ScaledLayout, qtm.Float8ScaledParams(scale, dtype))
@@ -219,6 +222,8 @@ def quantized_from_file(handle, entries, module, conf, shape, device, dtype, met
 
 def quantized_from_float(weight, fmt, **options):
     """Quantize a float weight into `fmt` (scale recomputed from the data, as ComfyUI set_weight)."""
+    if fmt == "float8_e5m2":
+        options = dict(options, fp8_dtype=torch.float8_e5m2)
     return qtm.QuantizedWeight.from_float(weight, layout_name(fmt), scale="recalculate", **options)
 
 
@@ -413,6 +418,10 @@ def native_linear(rows, qt, bias, fmt, input_scale=None, activation=None):
         return ops.gemm_i8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype, activation=activation)
     if layout is qtm.Float8ScaledLayout:
         qx, a_scale = _quantize_input(rows, True, 0, input_scale)
+        if qt._qdata.dtype == torch.float8_e5m2 and activation is not None:
+            # e5m2 weights have no fused epilogue: the linear output, rounded, then the activation
+            out = ops.gemm_fp8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype)
+            return apply_activation(out, activation).to(rows.dtype)
         return ops.gemm_fp8(qx, a_scale, qt._qdata, p.scale, bias, out_dtype=rows.dtype, activation=activation)
     if layout is qtm.UInt4GroupLayout:
         out = ops.gemm_w4a16(rows, qt._qdata, p.scale, p.zero, p.group_size, bias, out_dtype=rows.dtype)
@@ -589,10 +598,10 @@ def _template_from_shape(weight_meta, fmt, options):
         convrot, group = _convrot_options(options, k)
         params = qtm.Int8RowwiseParams(torch.empty(n, 1, dtype=torch.float32, device=meta), dtype, convrot, group)
         return qtm.QuantizedWeight(torch.empty(n, k, dtype=torch.int8, device=meta), qtm.Int8RowwiseLayout, params)
-    if fmt == "float8_e4m3fn":
+    if fmt in ("float8_e4m3fn", "float8_e5m2"):
+        code = torch.float8_e4m3fn if fmt == "float8_e4m3fn" else torch.float8_e5m2
         params = qtm.Float8ScaledParams(torch.empty((), dtype=torch.float32, device=meta), dtype)
-        return qtm.QuantizedWeight(torch.empty(n, k, dtype=torch.float8_e4m3fn, device=meta), qtm.Float8ScaledLayout,
-                                   params)
+        return qtm.QuantizedWeight(torch.empty(n, k, dtype=code, device=meta), qtm.Float8ScaledLayout, params)
     if fmt == "int4_asym_group":
         g = int(options.get("group_size", 128))
         if k % g:

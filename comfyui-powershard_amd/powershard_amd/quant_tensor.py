@@ -94,6 +94,7 @@ LAYOUTS = {cls.name: cls for cls in (Int8RowwiseLayout, Float8ScaledLayout, UInt
 QUANT_ALGOS = {
     "int8_tensorwise": {"comfy_tensor_layout": "Int8RowwiseLayout", "quantize_input": True},
     "float8_e4m3fn": {"comfy_tensor_layout": "Float8ScaledLayout", "quantize_input": True},
+    "float8_e5m2": {"comfy_tensor_layout": "Float8ScaledLayout", "quantize_input": True},
     "int4_asym_group": {"comfy_tensor_layout": "UInt4GroupLayout", "quantize_input": False},
 }
 
@@ -144,7 +145,8 @@ class QuantizedWeight:
         if self._layout_cls is Float8ScaledLayout:
             if gpu:
                 from . import ops
-                return ops.dequant_fp8(q.view(torch.uint8), p.scale, out_dtype=dtype)
+                return ops.dequant_fp8(q.view(torch.uint8), p.scale, out_dtype=dtype,
+                                       e5m2=q.dtype == torch.float8_e5m2)
             s = p.scale.float()
             w = q.float() * (s.reshape(-1, 1) if s.numel() > 1 else s.reshape(()))
             return w.to(dtype)
@@ -168,7 +170,8 @@ class QuantizedWeight:
 
         scale: None or "recalculate" re-derive the scale from the weight (the only mode used
         for weights, powershard/quant_linear.py:147-152).  Keyword options: convrot /
-        convrot_groupsize (int8), group_size (uint4).
+        convrot_groupsize (int8), group_size (uint4), fp8_dtype (float8_e4m3fn, the default, or
+        float8_e5m2).
         """
         layout = LAYOUTS[layout] if isinstance(layout, str) else layout
         dtype = weight.dtype if weight.is_floating_point() else torch.bfloat16
@@ -189,8 +192,12 @@ class QuantizedWeight:
             q = torch.round(w / s).clamp(-127, 127).to(torch.int8)
             return cls(q, layout, Int8RowwiseParams(s.contiguous(), dtype, convrot, group))
         if layout is Float8ScaledLayout:
-            s = w.abs().amax().clamp(min=1e-12) / 448.0
-            q = (w / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+            code = kw.get("fp8_dtype", torch.float8_e4m3fn)
+            if code not in (torch.float8_e4m3fn, torch.float8_e5m2):
+                raise ValueError(f"fp8 weights are float8_e4m3fn or float8_e5m2, not {code}")
+            top = torch.finfo(code).max            # 448 / 57344
+            s = w.abs().amax().clamp(min=1e-12) / top
+            q = (w / s).clamp(-top, top).to(code)
             return cls(q, layout, Float8ScaledParams(s.reshape(()).contiguous(), dtype))
         if layout is UInt4GroupLayout:
             group = int(kw.get("group_size", 128))
@@ -216,7 +223,7 @@ class QuantizedWeight:
                                               convrot_groupsize=p.convrot_groupsize)
         if self._layout_cls is UInt4GroupLayout:
             return QuantizedWeight.from_float(weight, self._layout_cls, scale, group_size=p.group_size)
-        return QuantizedWeight.from_float(weight, self._layout_cls, scale)
+        return QuantizedWeight.from_float(weight, self._layout_cls, scale, fp8_dtype=self._qdata.dtype)
 
     def __repr__(self):
         return f"QuantizedWeight({self._layout_cls.name}, shape={tuple(self.logical_shape())}, device={self.device})"

@@ -112,6 +112,16 @@ PSQ_API int psq_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale, co
                  int bias_dtype, void *y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
                  int64_t K, void *stream);
 
+/* FP8 with float8_e5m2 weights: e4m3fn activation codes (psq_quantize_rows_fp8) x e5m2 weight
+ * codes -> fp32 accumulate on the same f8f6f4 MFMA (A-operand format bf8), same epilogue and
+ * arguments as psq_gemm_fp8.  Replaces the native GEMM of comfy_quant "float8_e5m2"
+ * (powershard/quant_linear.py:32, 230-242), whose weights keep their e5m2 codes; the activations
+ * are quantized to e4m3fn, the finer of the two formats (3 mantissa bits against 2). */
+PSQ_API int psq_gemm_fp8_e5m2w(const uint8_t *a, int64_t lda, const float *a_scale,
+                 const uint8_t *w, int64_t ldw, const float *w_scale, int w_scale_per_row,
+                 const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy, int64_t M,
+                 int64_t N, int64_t K, void *stream);
+
 /* GEMM epilogue activations (the *_act entry points). */
 enum psq_activation {
     PSQ_ACT_NONE = 0,
@@ -226,6 +236,12 @@ PSQ_API int psq_dequant_i8_rows(const int8_t *q, const float *w_scale, int64_t N
 
 /* out = round_out(e4m3_to_f32(q) * scale[n or 0]). */
 PSQ_API int psq_dequant_fp8(const uint8_t *q, const float *w_scale, int w_scale_per_row, int64_t N,
+                    int64_t K, void *out, int out_dtype, void *stream);
+
+/* out = round_out(e5m2_to_f32(q) * scale[n or 0]): the float8_e5m2 weights' decode
+ * (powershard/quant_linear.py:387-404 for an F8_E5M2 file weight; comfy_quant "float8_e5m2",
+ * quant_linear.py:32).  e5m2_to_f32 is exact (the code is the high byte of an fp16). */
+PSQ_API int psq_dequant_e5m2(const uint8_t *q, const float *w_scale, int w_scale_per_row, int64_t N,
                     int64_t K, void *out, int out_dtype, void *stream);
 
 #ifdef __cplusplus

@@ -54,7 +54,11 @@ PINNING = {
                          "(test_quantize_fp8_*, test_quantize_nan_row_convention)",
     "gemm_i8_i32": "== numpy int64 matmul, also on selected rows; no overflow at the extremes",
     "epilogue_i32": "within 1 output ulp of float64 acc*a_s*w_s + bias; bf16 output == RNE of the fp32 value",
-    "gemm_fp8": "== float64 matmul of torch-decoded e4m3 operands",
+    "gemm_fp8": "== float64 matmul of torch-decoded e4m3 operands; with e5m2 weights, of torch-decoded "
+                "e4m3 activations and e5m2 weights (test_gemm_fp8_e5m2_weights_match_float64_matmul)",
+    "e5m2_to_f32 / dequant_fp8(e5m2)": "exhaustive over the 256 codes == torch's float8_e5m2 decode (NaN and inf "
+                                       "positions included); x scale then torch's cast "
+                                       "(test_e5m2_decode_exhaustive, test_dequant_e5m2_matches_torch_decode)",
     "dequant_fp8": "== torch's float8_e4m3fn decode x scale, then torch's cast (per tensor and per row; "
                    "test_dequant_fp8_matches_torch_decode)",
     "dequant_uint4": "== the nibble/zero/scale formula on torch tensors; quantize error <= s/2",
@@ -87,9 +91,11 @@ def lib():
         L.psq_or_gemm_i8_i32.argtypes = [P, I64, P, I64, P, I64, I64, I64, I64, P]
         L.psq_or_epilogue_i32.argtypes = [P, I64, P, P, I, P, I, P, I, I64, I64, I64, P]
         L.psq_or_gemm_fp8.argtypes = [P, I64, P, P, I64, P, I, P, I, P, I, I64, I64, I64, I64, P]
+        L.psq_or_gemm_fp8_e5m2w.argtypes = [P, I64, P, P, I64, P, I, P, I, P, I, I64, I64, I64, I64, P]
         L.psq_or_dequant_uint4.argtypes = [P, P, P, I64, I64, I, P, I]
         L.psq_or_dequant_i8_rows.argtypes = [P, P, I64, I64, I, P, I]
         L.psq_or_dequant_fp8.argtypes = [P, P, I, I64, I64, P, I]
+        L.psq_or_dequant_e5m2.argtypes = [P, P, I, I64, I64, P, I]
         L.psq_or_gemm_wonly.argtypes = [P, I, I64, P, I, P, P, I, P, I, I64, I64, I64, I64, P]
         L.psq_or_bf16_round.argtypes = [ctypes.c_float]
         L.psq_or_bf16_round.restype = ctypes.c_float
@@ -97,6 +103,8 @@ def lib():
         L.psq_or_f32_to_e4m3.restype = ctypes.c_uint8
         L.psq_or_e4m3_to_f32.argtypes = [ctypes.c_uint8]
         L.psq_or_e4m3_to_f32.restype = ctypes.c_float
+        L.psq_or_e5m2_to_f32.argtypes = [ctypes.c_uint8]
+        L.psq_or_e5m2_to_f32.restype = ctypes.c_float
         L.psq_or_f32_to_f16.argtypes = [ctypes.c_float]
         L.psq_or_f32_to_f16.restype = ctypes.c_uint16
         L.psq_or_f32_to_bf16.argtypes = [ctypes.c_float]
@@ -201,8 +209,11 @@ def epilogue_i32(c, a_scale, w_scale, bias=None, out_dtype=torch.bfloat16, row_i
     return y
 
 
-def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, row_ids=None):
-    """fp8 codes a [M,K], w [N,K] (uint8): y = round_out(fmaf(float(sum_f64), a_s*w_s, bias))."""
+def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, row_ids=None, w_e5m2=None):
+    """fp8 codes a [M,K] (e4m3fn), w [N,K] (e4m3fn, or e5m2 when w_e5m2; default: w's dtype):
+    y = round_out(fmaf(float(sum_f64), a_s*w_s, bias))."""
+    if w_e5m2 is None:
+        w_e5m2 = w.dtype == torch.float8_e5m2
     a, w = _cpu(a).view(torch.uint8), _cpu(w).view(torch.uint8)
     a_scale, w_scale = _cpu(a_scale).float(), _cpu(w_scale).float().reshape(-1)
     bias = None if bias is None else _cpu(bias)
@@ -210,10 +221,9 @@ def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, row_id
     M = a.shape[0] if rows is None else rows.numel()
     N, K = w.shape
     y = torch.empty(M, N, dtype=out_dtype)
-    lib().psq_or_gemm_fp8(_ptr(a), a.shape[1], _ptr(a_scale), _ptr(w), K, _ptr(w_scale),
-                          int(w_scale.numel() > 1), _ptr(bias),
-                          _DT[bias.dtype] if bias is not None else 0, _ptr(y), _DT[out_dtype], N,
-                          M, N, K, _ptr(rows))
+    fn = lib().psq_or_gemm_fp8_e5m2w if w_e5m2 else lib().psq_or_gemm_fp8
+    fn(_ptr(a), a.shape[1], _ptr(a_scale), _ptr(w), K, _ptr(w_scale), int(w_scale.numel() > 1), _ptr(bias),
+       _DT[bias.dtype] if bias is not None else 0, _ptr(y), _DT[out_dtype], N, M, N, K, _ptr(rows))
     return y
 
 
@@ -238,12 +248,22 @@ def dequant_i8_rows(q, scale, rot_group=0, out_dtype=torch.bfloat16):
     return out
 
 
-def dequant_fp8(q, scale, out_dtype=torch.bfloat16):
+def dequant_fp8(q, scale, out_dtype=torch.bfloat16, e5m2=None):
+    """round_out(decode(q) * s[n or 0]); q e4m3fn codes, or e5m2 when e5m2 (default: q's dtype)."""
+    if e5m2 is None:
+        e5m2 = q.dtype == torch.float8_e5m2
     q, scale = _cpu(q).view(torch.uint8), _cpu(scale).float().reshape(-1)
     N, K = q.shape
     out = torch.empty(N, K, dtype=out_dtype)
-    lib().psq_or_dequant_fp8(_ptr(q), _ptr(scale), int(scale.numel() > 1), N, K, _ptr(out), _DT[out_dtype])
+    fn = lib().psq_or_dequant_e5m2 if e5m2 else lib().psq_or_dequant_fp8
+    fn(_ptr(q), _ptr(scale), int(scale.numel() > 1), N, K, _ptr(out), _DT[out_dtype])
     return out
+
+
+def e5m2_to_f32(codes):
+    """The oracle's e5m2 decode of uint8 codes (from the format's definition)."""
+    return torch.tensor([lib().psq_or_e5m2_to_f32(int(c)) for c in codes.reshape(-1).tolist()],
+                        dtype=torch.float32).reshape(codes.shape)
 
 
 def gemm_wonly(x, wd, col_scale=None, bias=None, out_dtype=torch.bfloat16, row_ids=None):
@@ -290,6 +310,14 @@ def quantize_weight_fp8(w):
     w = w.float()
     scale = w.abs().max().clamp(min=1e-12) / 448.0
     q = (w / scale).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return q, scale.reshape(())
+
+
+def quantize_weight_e5m2(w):
+    """The same per-tensor recipe in e5m2 (max 57344): s = absmax.clamp(1e-12)/57344."""
+    w = w.float()
+    scale = w.abs().max().clamp(min=1e-12) / 57344.0
+    q = (w / scale).clamp(-57344, 57344).to(torch.float8_e5m2)
     return q, scale.reshape(())
 
 

@@ -28,6 +28,8 @@
  *  - fp8 e4m3fn (OCP) activation quantization per row: the same with 448 in place of 127,
  *    v = clamp(u * r, -448, 448), q = e4m3_rne(v).
  *  - int8 GEMM: acc[m][n] = sum_k a[m][k] * w[n][k] in int32 (exact, order free).
+ *  - fp8 GEMM: e4m3fn activation codes times e4m3fn or e5m2 weight codes, decoded exactly
+ *    and summed in double, then rounded to fp32 for the epilogue.
  *  - Epilogue (int8 and fp8): y = round_out(fmaf((float)acc, a_s[m] * w_s[n], bias[n])),
  *    bias = 0 when absent, round_out = RNE to bf16 / fp16, or identity for fp32.
  *  - uint4 asymmetric group weights (two per byte, low nibble = even k, group g along K,
@@ -120,6 +122,18 @@ static inline float e4m3_to_f32(uint8_t c)
     return s ? -v : v;
 }
 
+/* OCP FP8 E5M2 (bf8): bias 15, 2 mantissa bits, IEEE-style infinities (S.11111.00) and NaNs
+ * (S.11111.mm, mm != 0); subnormals m * 2^-16.  From the format's definition. */
+static inline float e5m2_to_f32(uint8_t c)
+{
+    uint32_t s = c >> 7, e = (c >> 2) & 0x1fu, m = c & 3u;
+    float v;
+    if (e == 0x1f) v = m ? NAN : INFINITY;
+    else if (e == 0) v = (float)m * 0x1p-16f;
+    else v = ldexpf(1.0f + (float)m * 0.25f, (int)e - 15);
+    return s ? -v : v;
+}
+
 /* round-to-nearest-even, saturating to +-448; NaN -> 0x7f. */
 static inline uint8_t f32_to_e4m3(float x)
 {
@@ -148,6 +162,7 @@ EXPORT uint16_t psq_or_f32_to_f16(float x) { return f32_to_f16(x); }
 EXPORT float psq_or_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
 EXPORT uint8_t psq_or_f32_to_e4m3(float x) { return f32_to_e4m3(x); }
 EXPORT float psq_or_e4m3_to_f32(uint8_t c) { return e4m3_to_f32(c); }
+EXPORT float psq_or_e5m2_to_f32(uint8_t c) { return e5m2_to_f32(c); }
 
 /* --------------------------------------------------------------- regular Hadamard */
 
@@ -351,15 +366,18 @@ EXPORT void psq_or_epilogue_i32(const int32_t *c, int64_t ldc, const float *a_sc
 }
 
 /* fp8 x fp8 GEMM, accumulated in double (exact products, nearly exact sum); the epilogue
- * then uses the double sum rounded to fp32.  Output rows follow row_ids. */
-EXPORT void psq_or_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale,
-                            const uint8_t *w, int64_t ldw, const float *w_scale,
-                            int w_scale_per_row, const void *bias, int bias_dtype, void *y,
-                            int out_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                            const int64_t *row_ids)
+ * then uses the double sum rounded to fp32.  Output rows follow row_ids.  The activations are
+ * e4m3fn codes; the weights e4m3fn (w_e5m2 = 0) or e5m2 codes (1). */
+static void gemm_fp8_any(const uint8_t *a, int64_t lda, const float *a_scale, const uint8_t *w,
+                         int64_t ldw, const float *w_scale, int w_scale_per_row, const void *bias,
+                         int bias_dtype, void *y, int out_dtype, int64_t ldy, int64_t M, int64_t N,
+                         int64_t K, const int64_t *row_ids, int w_e5m2)
 {
-    float lut[256];
-    for (int i = 0; i < 256; i++) lut[i] = e4m3_to_f32((uint8_t)i);
+    float alut[256], wlut[256];
+    for (int i = 0; i < 256; i++) {
+        alut[i] = e4m3_to_f32((uint8_t)i);
+        wlut[i] = w_e5m2 ? e5m2_to_f32((uint8_t)i) : e4m3_to_f32((uint8_t)i);
+    }
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < M; i++) {
         int64_t m = row_ids ? row_ids[i] : i;
@@ -367,12 +385,33 @@ EXPORT void psq_or_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale,
         for (int64_t n = 0; n < N; n++) {
             const uint8_t *wr = w + n * ldw;
             double acc = 0.0;
-            for (int64_t k = 0; k < K; k++) acc += (double)lut[ar[k]] * (double)lut[wr[k]];
+            for (int64_t k = 0; k < K; k++) acc += (double)alut[ar[k]] * (double)wlut[wr[k]];
             float ws = w_scale[w_scale_per_row ? n : 0];
             float b = bias ? load_act(bias, n, bias_dtype) : 0.0f;
             store_out(y, i * ldy + n, out_dtype, epilogue((float)acc, a_scale[m], ws, b));
         }
     }
+}
+
+EXPORT void psq_or_gemm_fp8(const uint8_t *a, int64_t lda, const float *a_scale,
+                            const uint8_t *w, int64_t ldw, const float *w_scale,
+                            int w_scale_per_row, const void *bias, int bias_dtype, void *y,
+                            int out_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                            const int64_t *row_ids)
+{
+    gemm_fp8_any(a, lda, a_scale, w, ldw, w_scale, w_scale_per_row, bias, bias_dtype, y, out_dtype,
+                 ldy, M, N, K, row_ids, 0);
+}
+
+/* The same with e5m2 weight codes. */
+EXPORT void psq_or_gemm_fp8_e5m2w(const uint8_t *a, int64_t lda, const float *a_scale,
+                                  const uint8_t *w, int64_t ldw, const float *w_scale,
+                                  int w_scale_per_row, const void *bias, int bias_dtype, void *y,
+                                  int out_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                  const int64_t *row_ids)
+{
+    gemm_fp8_any(a, lda, a_scale, w, ldw, w_scale, w_scale_per_row, bias, bias_dtype, y, out_dtype,
+                 ldy, M, N, K, row_ids, 1);
 }
 
 /* -------------------------------------------------------- uint4 group weights */
@@ -431,6 +470,16 @@ EXPORT void psq_or_dequant_fp8(const uint8_t *q, const float *scale, int per_row
     for (int64_t n = 0; n < N; n++)
         for (int64_t k = 0; k < K; k++)
             store_out(out, n * K + k, out_dtype, e4m3_to_f32(q[n * K + k]) * scale[per_row ? n : 0]);
+}
+
+/* e5m2 weights: out = round_out(e5m2(q) * s[n or 0]). */
+EXPORT void psq_or_dequant_e5m2(const uint8_t *q, const float *scale, int per_row, int64_t N,
+                                int64_t K, void *out, int out_dtype)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; n++)
+        for (int64_t k = 0; k < K; k++)
+            store_out(out, n * K + k, out_dtype, e5m2_to_f32(q[n * K + k]) * scale[per_row ? n : 0]);
 }
 
 /* Weight-only GEMM over an already dequantized weight wd [N, K] (in wd_dtype), activations

@@ -217,6 +217,47 @@ def test_gemm_fp8_matches_float64_matmul():
     assert torch.allclose(y, ref, rtol=2e-7, atol=0)
 
 
+def test_gemm_fp8_e5m2_weights_match_float64_matmul():
+    """e4m3 activations x e5m2 weights: the double sum of the torch-decoded operands."""
+    g = torch.Generator().manual_seed(18)
+    a = (torch.randn(17, 256, generator=g) * 50).clamp(-448, 448).to(torch.float8_e4m3fn)
+    w = (torch.randn(23, 256, generator=g) * 3000).clamp(-57344, 57344).to(torch.float8_e5m2)
+    sa, sw = torch.rand(17, generator=g), torch.rand(23, generator=g) * 1e-4
+    y = oracle.gemm_fp8(a, sa, w, sw, None, out_dtype=torch.float32)
+    exact = a.double() @ w.double().T
+    ref = (exact.float().double() * (sa.double()[:, None] * sw.double()[None, :].float().double())).float()
+    assert torch.allclose(y, ref, rtol=2e-7, atol=0)
+    # the weights' format matters: read as e4m3 the same bytes give another product
+    y43 = oracle.gemm_fp8(a, sa, w.view(torch.uint8), sw, None, out_dtype=torch.float32, w_e5m2=False)
+    assert not torch.allclose(y43, y)
+
+
+def test_e5m2_decode_exhaustive():
+    """The oracle's e5m2 decode (written from the format's definition) is torch's on all 256 codes."""
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    got = oracle.e5m2_to_f32(codes)
+    ref = codes.view(torch.float8_e5m2).float()
+    assert torch.equal(torch.isnan(got), torch.isnan(ref))
+    ok = ~torch.isnan(ref)
+    assert torch.equal(got[ok], ref[ok])
+    assert torch.isinf(ref).sum() == 2 and torch.isnan(ref).sum() == 6
+    assert got[0x01] == 2.0 ** -16 and got[0x7B] == 57344.0
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequant_e5m2_matches_torch_decode(per_row, out_dtype):
+    """round_out(e5m2(q) * s): torch's float8_e5m2 decode times the fp32 scale, then torch's cast."""
+    g = torch.Generator().manual_seed(43)
+    codes = torch.randint(0, 256, (29, 80), generator=g, dtype=torch.uint8)
+    codes[(codes & 0x7C) == 0x7C] = 0x7B          # finite codes only
+    s = torch.rand(29, generator=g) * 1e-2 + 1e-4 if per_row else torch.tensor(2.7e-3)
+    got = oracle.dequant_fp8(codes.view(torch.float8_e5m2), s, out_dtype)
+    ref = (codes.view(torch.float8_e5m2).float() * (s[:, None] if per_row else s)).to(out_dtype)
+    assert torch.equal(got.view(torch.int16) if out_dtype != torch.float32 else got,
+                       ref.view(torch.int16) if out_dtype != torch.float32 else ref)
+
+
 def test_gemm_wonly_matches_float64_matmul():
     g = torch.Generator().manual_seed(9)
     x = torch.randn(11, 384, generator=g).to(torch.bfloat16)

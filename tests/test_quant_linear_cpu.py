@@ -169,7 +169,7 @@ def _save(tmp_path, tensors, conf=None, name="m"):
 def _table(path):
     from safetensors import safe_open
     code = {torch.float32: "F32", torch.float16: "F16", torch.bfloat16: "BF16", torch.int8: "I8",
-            torch.uint8: "U8", torch.float8_e4m3fn: "F8_E4M3"}
+            torch.uint8: "U8", torch.float8_e4m3fn: "F8_E4M3", torch.float8_e5m2: "F8_E5M2"}
     with safe_open(str(path), framework="pt") as f:
         table = {k: {"key": k, "dtype": code[f.get_tensor(k).dtype], "shape": list(f.get_tensor(k).shape)}
                  for k in f.keys()}
@@ -209,6 +209,51 @@ def test_fp8_scaled_file(tmp_path):
                                 "m.weight", "cpu")
     torch.testing.assert_close(out, q.float() * scale)
     torch.testing.assert_close(plain, q.float() * scale)
+
+
+def test_e5m2_scaled_file_module_as_file(tmp_path):
+    """A float8_e5m2 comfy_quant module (F8_E5M2 weight, F32 per-tensor weight_scale) loads as_file:
+    its qbytes keep the e5m2 codes, unpack rebuilds them, and the dequantize branch equals the
+    reference's decode q * s (the plain formula of powershard/quant_formats.py:95-103)."""
+    from safetensors import safe_open
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(32, 256, generator=g)
+    scale = w.abs().max() / 57344.0
+    q = (w / scale).to(torch.float8_e5m2)
+    conf = {"format": "float8_e5m2"}
+    path = _save(tmp_path, {"m.weight": q, "m.weight_scale": scale.reshape(()), "m.bias": torch.zeros(32)}, conf)
+    table, confs = _table(path)
+    assert confs == {"m": conf}
+    with safe_open(str(path), framework="pt") as f:
+        out = qf.dequantize_module(f, qf.module_entries(table, "m"), "m", conf, [32, 256], torch.device("cpu"),
+                                   torch.float32)
+    torch.testing.assert_close(out, q.float() * scale)
+    net = nn.ModuleDict({"m": nn.Linear(256, 32).to(torch.bfloat16)})
+    report = ql.install_quant_linears(net, table, "as_file", "dequantize", None, torch.bfloat16, "cpu")
+    layer = net["m"]
+    assert report["modules"]["float8_e5m2"]["source"] == {"file": 1}
+    with safe_open(str(path), framework="pt") as f:
+        full, used = ql.build_bytes(layer, f, "cpu")
+    assert used == {"m.weight", "m.weight_scale", "m.comfy_quant"}
+    qt = ql.unpack(full, layer._ps_qplan, torch.bfloat16)
+    assert qt._qdata.dtype == torch.float8_e5m2 and torch.equal(qt._qdata.view(torch.uint8), q.view(torch.uint8))
+    layer.qbytes = nn.Parameter(full, requires_grad=False)
+    layer.bias = None
+    x = torch.randn(5, 256, dtype=torch.bfloat16)
+    ref = torch.nn.functional.linear(x, (q.float() * scale).to(torch.bfloat16))
+    torch.testing.assert_close(layer(x), ref, atol=0, rtol=0)
+
+
+def test_e5m2_requantize_keeps_the_format():
+    """A LoRA merge re-quantizes an e5m2 weight into e5m2 (scale absmax / 57344), as the template."""
+    g = torch.Generator().manual_seed(4)
+    w = torch.randn(16, 128, generator=g)
+    qt = ql.quantized_from_float(w, "float8_e5m2")
+    assert qt._qdata.dtype == torch.float8_e5m2
+    assert torch.equal(qt._params.scale, w.abs().max() / 57344.0)
+    again = ql.requantize_like(qt, w * 2, "float8_e5m2")
+    assert again._qdata.dtype == torch.float8_e5m2
+    torch.testing.assert_close(again.dequantize().float(), (w * 2).to(torch.bfloat16).float(), rtol=0.13, atol=1e-6)
 
 
 def test_convrot_file_module_loads_as_file_and_matches_dequantize_rows(tmp_path):
