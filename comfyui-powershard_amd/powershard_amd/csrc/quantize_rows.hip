@@ -318,10 +318,12 @@ template <int DT, bool FP8>
 int launch_quant(const void *x, int64_t M, int64_t K, int64_t ldx, int rotk,
                  const float *static_scale, uint8_t *q, int64_t ldq, float *scale, hipStream_t st)
 {
-    // chunks per thread: 1 up to 16384 elements, else 2 (up to 32768); one row per workgroup
-    // (two rows side by side measured slower: 160 vs 138 us at 32760 x 5120)
+    // chunks per thread: 1 up to 8192 elements, else 2 (up to 32768); one row per workgroup
+    // (two rows side by side measured slower: 160 vs 138 us at 32760 x 5120).  Past 8192 the
+    // smaller workgroups of two chunks per thread overlap their loads, reduction barrier and
+    // stores better: 32760 x 13824 270 -> 238 us; at K = 5120 one chunk stays ahead (95 vs 100 us).
     const int64_t chunks16 = K / kElemsPerThread;
-    const int P = chunks16 <= kMaxThreads ? 1 : 2;
+    const int P = chunks16 <= 512 ? 1 : 2;
     const int threads = (int)((chunks16 + P - 1) / P + 63) / 64 * 64;
     const uint16_t *xp = (const uint16_t *)x;
     if (P == 2) return launch_quant_p<DT, FP8, 2, 1>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st);

@@ -83,12 +83,15 @@ QUANT_CASES = [
     (37, 512, 16, torch.bfloat16),
     (5, 1024, 1024, torch.bfloat16),
     (9, 13824, 256, torch.bfloat16),
+    (4, 9216, 1024, torch.float16),
     (3, 64, 0, torch.bfloat16),
     (17, 256, 64, torch.float16),
     (8, 4096, 4, torch.float16),
     (1, 16, 0, torch.bfloat16),
     (300, 2048, 256, torch.bfloat16),
-    # two 16-element chunks per thread (K > 16384): Qwen3-VL down_proj K, the maximum, just over
+    # two 16-element chunks per thread (K > 8192): the Wan FFN down K, an odd chunk count with a
+    # partial last wave, the Qwen3-VL down_proj K, the maximum, just over 16384
+    (9, 8208, 16, torch.bfloat16),
     (7, 25600, 256, torch.bfloat16),
     (3, 32768, 1024, torch.float16),
     (5, 16400, 16, torch.bfloat16),
