@@ -301,9 +301,13 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     // Scale / zero blocks (uint4, groups per row a multiple of SZG, 16-byte aligned tables): a
     // block of SZG groups is loaded once, with the first stage of the block (or of the workgroup's
     // K range), instead of a 2-byte scattered load per stage.  Otherwise the per-stage loads.
-    const bool szblk = WK == W_UINT4 && G % SZG == 0 && ((uintptr_t)wa.scale16 % 16) == 0 &&
+    // (stages per group a power of two, so that a stage's group and block are shifts and masks:
+    // the per-stage bookkeeping sits between the MFMAs)
+    const bool szblk = WK == W_UINT4 && G % SZG == 0 && (spg & (spg - 1)) == 0 && ((uintptr_t)wa.scale16 % 16) == 0 &&
                        ((uintptr_t)wa.zero16 % 16) == 0;
-    const unsigned spb = spg * SZG;                           // stages per scale block
+    const int spg_sh = spg ? __builtin_ctz(spg) : 0;          // log2 stages per group (szblk)
+    static_assert(SZG == 8, "scale blocks of 8 groups");
+    const unsigned spb_mask = (spg << 3) - 1;                 // stages per scale block - 1
     uint8_t *const szbuf = smem + NSTAGE * SLOT;
     const uint8_t *xb = (const uint8_t *)(x + (int64_t)m0 * ldx);
     const uint8_t *wb = wa.wq + (int64_t)n0 * wld;
@@ -326,8 +330,8 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             const bool zero = wave >= 4;
             if (szblk) {
                 // the block of the stage's group, with the block's first stage (or the range's)
-                if (kt == kb || (unsigned)kt % spb == 0) {
-                    const unsigned blk = (unsigned)kt / spb;
+                if (kt == kb || ((unsigned)kt & spb_mask) == 0) {
+                    const unsigned blk = (unsigned)kt >> (spg_sh + 3);
                     const int64_t gi = (int64_t)scol * G + SZG * blk;
                     __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
                                                      (lds_ptr)(szbuf + (blk & 1) * SZB_BYTES + 1024 * wave), 16, 0, 0);
@@ -363,7 +367,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
             if constexpr (WK == W_UINT4) {
                 if (szblk) {
-                    const unsigned g = (unsigned)kt / spg;
+                    const unsigned g = (unsigned)kt >> spg_sh;
                     const uint8_t *zb = szbuf + ((g / SZG) & 1) * SZB_BYTES + 16 * n + 2 * (g % SZG);
                     r.s[j] = f16_to_f32(*(const uint16_t *)zb);
                     r.z[j] = -(f16_to_f32(*(const uint16_t *)(zb + BN * 16)) * r.s[j]);   // -z s
