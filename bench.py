@@ -13,8 +13,9 @@ its average launch time, timed with HIP events on its stream around a loop of ba
 launches on the headline's quantized input.  `cpu_baseline` is the reference's own CPU path for
 the same layer -- QuantLinear's dequantize branch: dequantize_rows (q * s, ConvRot inverse) and
 F.linear in bf16 on torch-CPU (powershard/quant_linear.py:219-220, operations.py:84-93) -- on a
-bounded row sample, on all of this process's CPU threads and on one, with the c0 / c2 layers and
-one Wan-14B block (x40, derived) beside it and the C oracle's quantized forward as a second figure.
+bounded row sample, on all of this process's CPU threads and on one, with the int8 weight-only
+(1024 x 5120 -> 5120) and uint4 g128 (512 x 5120 -> 25600) layers and one Wan-14B block (x40,
+derived) beside it and the C oracle's quantized forward as a second figure.
 
 `extra` carries the other shapes, each with a sampled-row check against the oracle: the int4
 (W4A16) text-encoder MLP at M=512 with an M sweep, the fp8 QKV projection, the int8 weight-only
@@ -321,23 +322,23 @@ def _uint4_dequant(wq, s, z, g):
 
 
 def cpu_inputs(sample):
-    """CPU copies of the c0, c2 and one-Wan-block (c4) layers, built on the GPU with the seeds of
+    """CPU copies of the int8 weight-only, uint4 and one-Wan-block layers, built on the GPU with the seeds of
     their GPU workloads, and their activation rows."""
     import torch
     c = {}
     layer, qt, b = quant_layer(5120, 5120, "int8", 0)
-    c["c0"] = dict(q=qt._qdata.cpu(), s=qt._params.scale.cpu(), b=b.cpu(),
-                   x=activations(1024, 5120, 0, outlier_scale=1.0).cpu())
+    c["int8_wonly"] = dict(q=qt._qdata.cpu(), s=qt._params.scale.cpu(), b=b.cpu(),
+                           x=activations(1024, 5120, 0, outlier_scale=1.0).cpu())
     layer, qt, b = quant_layer(5120, 25600, "int4", 2, seed=1002, opts={"group_size": 128})
     p = qt._params
-    c["c2"] = dict(q=qt._qdata.cpu(), s=p.scale.cpu(), z=p.zero.cpu(), b=b.cpu(),
+    c["uint4"] = dict(q=qt._qdata.cpu(), s=p.scale.cpu(), z=p.zero.cpu(), b=b.cpu(),
                    x=activations(512, 5120, 2, outlier_scale=1.0).cpu())
     opts = {"convrot": True, "convrot_groupsize": 256}
     blk = []
     for i, (k_, n_) in enumerate(((5120, 5120),) * 4 + ((5120, 13824), (13824, 5120))):
         layer, qt, b = quant_layer(k_, n_, "int8", 4, seed=1004 + i + 1, opts=opts)
         blk.append(dict(q=qt._qdata.cpu(), s=qt._params.scale.cpu(), b=b.cpu()))
-    c["c4"] = dict(layers=blk, x=activations(256, 5120, 4, outlier_scale=50.0, student_t=True).cpu(),
+    c["wan_block"] = dict(layers=blk, x=activations(256, 5120, 4, outlier_scale=50.0, student_t=True).cpu(),
                    h=activations(256, 13824, 104, outlier_scale=50.0, student_t=True).cpu())
     del layer, qt
     torch.cuda.empty_cache()
@@ -346,7 +347,8 @@ def cpu_inputs(sample):
 
 def cpu_baseline(sample, inputs, target_s):
     """The reference's CPU path (QuantLinear dequantize branch on torch-CPU) for the headline layer on
-    all threads and on one, the c0 / c2 layers and one Wan-14B block (x40, derived), and the C
+    all threads and on one, the int8 weight-only and uint4 layers and one Wan-14B block (x40,
+    derived), and the C
     oracle's quantized W8A8 forward as a second figure."""
     import torch
     import oracle
@@ -363,20 +365,20 @@ def cpu_baseline(sample, inputs, target_s):
         torch.set_num_threads(threads)
     log(f"[bench] cpu reference path, 1 thread: {one['tops'] * 1e3:.1f} GOPS")
     configs = {}
-    c0 = inputs["c0"]
-    configs["c0_int8_weight_only_1024x5120x5120"] = reference_cpu_forward(
-        _rowwise_dequant(c0["q"], c0["s"]), c0["x"], 1024, c0["b"], target_s)
-    c2 = inputs["c2"]
-    configs["c2_uint4_g128_512x5120x25600"] = reference_cpu_forward(
-        _uint4_dequant(c2["q"], c2["s"], c2["z"], 128), c2["x"], 512, c2["b"], target_s)
-    c4 = inputs["c4"]
+    wonly = inputs["int8_wonly"]
+    configs["int8_weight_only_1024x5120x5120"] = reference_cpu_forward(
+        _rowwise_dequant(wonly["q"], wonly["s"]), wonly["x"], 1024, wonly["b"], target_s)
+    u4 = inputs["uint4"]
+    configs["uint4_g128_512x5120x25600"] = reference_cpu_forward(
+        _uint4_dequant(u4["q"], u4["s"], u4["z"], 128), u4["x"], 512, u4["b"], target_s)
+    blk = inputs["wan_block"]
     block_s, block_ops = 0.0, 0.0
-    for i, lay in enumerate(c4["layers"]):
-        xr = c4["h"] if i == 5 else c4["x"]
+    for i, lay in enumerate(blk["layers"]):
+        xr = blk["h"] if i == 5 else blk["x"]
         r = reference_cpu_forward(_convrot_dequant(lay["q"], lay["s"], 256), xr, 32760, lay["b"], target_s / 3)
         block_s += r["forward_s"]
         block_ops += 2.0 * 32760 * lay["q"].shape[0] * lay["q"].shape[1]
-    configs["c4_wan14b_40_blocks_derived"] = dict(block_s=block_s, total_s=40 * block_s,
+    configs["wan14b_40_blocks_derived"] = dict(block_s=block_s, total_s=40 * block_s,
                                                   tops=block_ops / block_s / 1e12,
                                                   note="one block timed (6 layers, row samples), x40")
     for k, v in configs.items():

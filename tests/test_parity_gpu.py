@@ -1,5 +1,5 @@
 """GPU parity cases beyond the per-kernel suite: the reference's own QuantLinear criterion, the
-weight-only kernels at the c2 text-encoder shape (their 256-row tile instantiation), the on-disk
+weight-only kernels at the text-encoder MLP shape 512 x 5120 -> 25600 (their 256-row tile instantiation), the on-disk
 int8 ConvRot module through the kernels, NaN rows, and the dequantize kernels at K = 25600.
 
 * ``test_native_matches_dequantize_branch``: the reference checks QuantLinear against
@@ -115,7 +115,7 @@ def test_quantlinear_nan_row_propagates(gpu, weight_format, opts):
     assert torch.isfinite(y[[0, 1, 2, 3, 4, 6, 7]]).all()
 
 
-# ------------------------------------------ weight-only GEMMs at the c2 shape (256-row tiles)
+# ------------------- weight-only GEMMs at the text-encoder MLP shape (256-row tiles)
 def _wonly_rows(x, wd, b, rows):
     return oracle.gemm_wonly(x, wd, None, b, out_dtype=torch.float32, row_ids=rows)
 
@@ -163,8 +163,8 @@ def test_gemm_w8a16_256_row_tiles(gpu, N):
     assert_fp32_path(y32, yb, ref, f"w8a16 256-row tiles N={N}")
 
 
-def test_c2_int4_text_encoder_mlp(gpu):
-    """The c2 workload itself: uint4 g128 weights 25600 x 5120, M = 512 prompt tokens, through the
+def test_int4_text_encoder_mlp_512x5120x25600(gpu):
+    """The text-encoder workload itself: uint4 g128 weights 25600 x 5120, M = 512 prompt tokens, through the
     QuantLinear module; 256 sampled rows x all 25600 columns against the oracle."""
     from powershard_amd import ops
     M, K, N = 512, 5120, 25600
@@ -179,7 +179,7 @@ def test_c2_int4_text_encoder_mlp(gpu):
     rows = _sample_rows(M, 256, 76)
     wd = oracle.dequant_uint4(qt._qdata, p.scale, p.zero, 128, out_dtype=torch.bfloat16)
     ref = _wonly_rows(x, wd, b, rows)
-    assert_fp32_path(y32[rows], yb[rows], ref, "c2 W4A16 512x5120->25600")
+    assert_fp32_path(y32[rows], yb[rows], ref, "W4A16 512x5120->25600")
 
 
 # ----------------------------------------------- on-disk int8 ConvRot module (comfy_quant)
