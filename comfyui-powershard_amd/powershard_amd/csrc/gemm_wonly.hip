@@ -821,7 +821,7 @@ constexpr int NW = 8, ROWS = 16 * NW;                 // waves; weight rows per 
 constexpr int B = 256;                                // k per block
 constexpr int WBYTES = 16 * B / 2;                    // a wave's nibbles per block (2 KB)
 constexpr int WSLOT = WBYTES + 256;                   // + its scale / zero words
-constexpr int MAXM = 4;
+constexpr int MAXM = 8;
 constexpr int LOADS = 3;                              // ring loads per wave and block
 __host__ __device__ inline int64_t xrow(int64_t K) { return 2 * K + 16; } // padded activation row in LDS (bytes)
 inline int64_t lds_bytes(int64_t M, int64_t K, int D) { return M * xrow(K) + (int64_t)NW * D * WSLOT; }

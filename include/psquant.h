@@ -161,7 +161,8 @@ PSQ_API int psq_gemm_fp8_act(const uint8_t *a, int64_t lda, const float *a_scale
  * fp32 accumulation; y = round_out(acc + bias).  Replaces the int4 F.linear dispatch
  * (powershard/quant_linear.py:239, weight-only formats) and matches the dequantize
  * branch F.linear(rows, qt.dequantize().to(bf16), bias) (quant_linear.py:219-220).
- * The decode kernel (M <= 4, group_size a multiple of 128, K a multiple of 512), the
+ * The decode kernel (M <= 8 whose activations fit in LDS beside the weight rings, group_size
+ * a multiple of 128, K a multiple of 512), the
  * weight-streaming kernel (M <= 64, group_size a multiple of 128) and the tiled kernel (M > 64)
  * form w = round_bf16(fmaf(q, scale, -(zero * scale))), which differs from the formula above by
  * one bf16 ulp on about 2^-16 of the weights; all are within the fp32-accumulation bar.

@@ -348,13 +348,15 @@ def test_gemm_w4a16_unsplit_entry_point(gpu):
     assert (y.cpu() - ref).abs().max().item() <= 1e-2 * rms
 
 
-# ------------------------------------------------------------ W4A16 decode kernel (M <= 4)
+# ------------------------------------------------------------ W4A16 decode kernel (M <= 8)
 @pytest.mark.parametrize("M,N,K,gs", [(1, 25600, 5120, 128), (2, 2600, 5120, 128), (3, 389, 1024, 256),
-                                      (4, 1000, 3072, 128), (1, 130, 25600, 128), (4, 256, 512, 512)])
+                                      (4, 1000, 3072, 128), (1, 130, 25600, 128), (4, 256, 512, 512),
+                                      (5, 777, 5120, 128), (8, 25600, 5120, 128), (6, 300, 12800, 256),
+                                      (7, 129, 1024, 128)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemm_w4a16_decode(gpu, M, N, K, gs, xdt):
-    """M <= 4 with K % 512 == 0 runs the barrier-free decode kernel (activations in LDS, a private
-    weight ring per wave); same bar as the other weight-only paths."""
+    """M <= 8 with K % 512 == 0 (the activations fitting in LDS) runs the barrier-free decode kernel
+    (activations in LDS, a private weight ring per wave); same bar as the other weight-only paths."""
     from powershard_amd import ops
     x = heavy_rows(M, K, seed=110 + M, outlier_frac=0, dtype=xdt)
     w = torch.randn(N, K, generator=seeded(111)) * 0.02
