@@ -409,8 +409,9 @@ def cpu_baseline(sample, inputs, target_s):
 def extra_int4(args):
     """W4A16 uint4 g128 Qwen3-VL-32B text-encoder MLP, K=5120 -> N=25600; M sweep.  Weights rotate
     over 12 distinct copies (12 x 69.6 MB = 835 MB, over three times the 256 MB Infinity Cache), so
-    each launch streams its weights from HBM; each M is timed as a loop of back-to-back kernel
-    launches with events around the loop.  M = 1 and M = 512 are checked on sampled rows."""
+    each launch streams its weights from HBM; each M is timed as a loop of 100 back-to-back kernel
+    launches with events around the loop, after 400 untimed ones.  M = 1 and M = 512 are checked on
+    sampled rows."""
     import torch
     import oracle
     from powershard_amd import ops
@@ -426,7 +427,9 @@ def extra_int4(args):
             q, sc, z, b = ws[it[0] % copies]
             ops.gemm_w4a16(x, q, sc, z, 128, b)
             it[0] += 1
-        kms = untimed_kernel_ms(step, max(args.steps, 24), max(args.warmup, 12))
+        # a serving loop's steady state: the shader clock of these short launches settles over
+        # ~10 ms of back-to-back launches (M=1: 26 us over the first 500 launches, 24 us after)
+        kms = untimed_kernel_ms(step, max(args.steps, 100), max(args.warmup, 400))
         wbytes = N * K // 2 + 2 * 2 * N * (K // 128)
         algo_bytes = wbytes + M * K * 2 + M * N * 2
         flops = 2.0 * M * N * K
