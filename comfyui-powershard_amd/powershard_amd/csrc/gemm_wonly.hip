@@ -62,15 +62,6 @@ constexpr int SK_BLOCK = 128;                  // k per block: 4 lane groups x 3
 
 // The four bytes of w as floats: v_cvt_f32_ubyte0..3, one instruction each (the compiler would
 // otherwise extract each nibble-masked byte with a bitfield op first).
-__device__ __forceinline__ float ubyte_to_f32(uint32_t w, int e)
-{
-    float f;
-    if (e == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(w));
-    else if (e == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(w));
-    else if (e == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(w));
-    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(w));
-    return f;
-}
 __device__ __forceinline__ void ubytes_to_f32(uint32_t w, float (&f)[4])
 {
     asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f[0]) : "v"(w));
@@ -78,6 +69,44 @@ __device__ __forceinline__ void ubytes_to_f32(uint32_t w, float (&f)[4])
     asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f[2]) : "v"(w));
     asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f[3]) : "v"(w));
 }
+
+// uint4 dequantization without an int -> float step.  A nibble q alone in a 16-bit half is the
+// fp16 subnormal q * 2^-24, and v_fma_mix_f32 takes an fp16 operand as is, so
+//   fma_mix(q * 2^-24, s * 2^24, c) = fmaf(q, s, c)
+// exactly: s * 2^24 is an exact fp32 scaling of the fp16 scale and the fma's product is exact
+// (checked on gfx950 for all q against fmaf over 2^20 fp16 scales, subnormal ones included).
+// The eight nibbles of a word (nibble i = k offset i) are split into four such pairs with 7 ops,
+// then one fma_mix per weight: 19 VALU ops per 8 weights with the packs, against 23 for
+// v_cvt_f32_ubyte + v_fma_f32.
+struct Nib4 { uint32_t a, b, c, d; };   // halves (lo, hi): a = k (0, 4), b = (1, 5), c = (2, 6), d = (3, 7)
+__device__ __forceinline__ Nib4 nib_split(uint32_t p)
+{
+    return Nib4{p & 0x000f000fu, (p >> 4) & 0x000f000fu, (p >> 8) & 0x000f000fu, (p >> 12) & 0x000f000fu};
+}
+__device__ __forceinline__ float mix_lo(uint32_t h2, float s24, float c)
+{
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s24), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float mix_hi(uint32_t h2, float s24, float c)
+{
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s24), "v"(c));
+    return r;
+}
+// packed weights of k offsets 2e, 2e + 1: round_16(fmaf(q, s, c)) each, s24 = s * 2^24
+template <int XDT>
+__device__ __forceinline__ uint32_t dq_pair_u4(const Nib4 &v, int e, float s24, float c)
+{
+    switch (e) {
+    case 0: return pack_half2<XDT>(mix_lo(v.a, s24, c), mix_lo(v.b, s24, c));
+    case 1: return pack_half2<XDT>(mix_lo(v.c, s24, c), mix_lo(v.d, s24, c));
+    case 2: return pack_half2<XDT>(mix_hi(v.a, s24, c), mix_hi(v.b, s24, c));
+    default: return pack_half2<XDT>(mix_hi(v.c, s24, c), mix_hi(v.d, s24, c));
+    }
+}
+constexpr float kTwo24 = 16777216.0f;
 
 template <int XDT, int WK, int MT>
 __global__ void __launch_bounds__(NTHREADS)
@@ -355,8 +384,8 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         return __builtin_bit_cast(XV, *(const v4i *)(smem + slot * SLOT + r * XROW + ((c ^ xsw(r)) << 4)));
     };
     // the lane's packed weights of a stage (its 32 k of each of its two columns) and, for uint4,
-    // the columns' group scale s and -z s: a weight is round_16(fmaf(q, s, -z s)), one VALU op
-    // (as in the streaming kernel)
+    // the columns' group scale s (held as s 2^24) and -z s: a weight is round_16(fmaf(q, s, -z s)),
+    // one fma_mix per weight (dq_pair_u4)
     struct WRaw { v4i w[TN][RB / 32]; float s[TN], z[TN]; };
     auto read_w = [&](int slot, int kt, WRaw &r) {
         const uint8_t *sl = smem + slot * SLOT + XBYTES;
@@ -366,15 +395,18 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
 #pragma unroll
             for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
             if constexpr (WK == W_UINT4) {
+                float sv, zv;
                 if (szblk) {
                     const unsigned g = (unsigned)kt >> spg_sh;
                     const uint8_t *zb = szbuf + ((g / SZG) & 1) * SZB_BYTES + 16 * n + 2 * (g % SZG);
-                    r.s[j] = f16_to_f32(*(const uint16_t *)zb);
-                    r.z[j] = -(f16_to_f32(*(const uint16_t *)(zb + BN * 16)) * r.s[j]);   // -z s
+                    sv = f16_to_f32(*(const uint16_t *)zb);
+                    zv = f16_to_f32(*(const uint16_t *)(zb + BN * 16));
                 } else {
-                    r.s[j] = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
-                    r.z[j] = -(f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n)) * r.s[j]);   // -z s
+                    sv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
+                    zv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n));
                 }
+                r.s[j] = sv * kTwo24;     // s 2^24 for the fp16-subnormal nibbles (dq_pair_u4)
+                r.z[j] = -(zv * sv);      // -z s
             } else {
                 r.s[j] = 1.0f;
                 r.z[j] = 0.0f;
@@ -384,11 +416,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     // pair e (k = 32 h + 8 t + 2e, +1) of column tile j's weights in k-step t, packed
     auto dq_pair = [&](const WRaw &r, int j, int t, int e) -> uint32_t {
         if constexpr (WK == W_UINT4) {
-            const uint32_t p = (uint32_t)r.w[j][0][t];
-            float q[2];
-            q[0] = ubyte_to_f32(p & 0x0f0f0f0fu, e);           // even k: low nibble of byte e
-            q[1] = ubyte_to_f32((p >> 4) & 0x0f0f0f0fu, e);    // odd k: high nibble
-            return pack2<XDT>(__builtin_fmaf(q[0], r.s[j], r.z[j]), __builtin_fmaf(q[1], r.s[j], r.z[j]));
+            return dq_pair_u4<XDT>(nib_split((uint32_t)r.w[j][0][t]), e, r.s[j], r.z[j]);
         } else {
             const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
             const int sh = 16 * (e & 1);
@@ -603,8 +631,8 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
 //  * The lane dequantizes its 32 weights per block, w = round_16(fmaf(q, s, -z s)): one fma per
 //    weight where the other paths compute (q - z) * s, so a weight can differ from theirs by one
 //    16-bit ulp (when the two fp32 values straddle a rounding boundary, about 2^-16 of the
-//    weights) -- far inside the fp32-accumulation bar.  The VALU work per weight (nibble convert,
-//    fma, half a pack) is what bounds this kernel at small M.
+//    weights) -- far inside the fp32-accumulation bar.  The VALU work per weight (7/8 of an op to
+//    split the nibbles, one fma_mix, half a pack: dq_pair_u4) is what bounds this kernel at small M.
 //  * MFMA 16x16x32 with the activations as the A operand: lane (n = l & 15, h = l >> 4) holds
 //    output column n (its weight row) and rows 4 h .. 4 h + 3 of each 16-row tile.  Lane group h
 //    carries k = 32 h + 8 t .. + 7 of the block in k-step t for both operands.
@@ -723,8 +751,9 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
         }
         const int si = (nr << (KHV - 1)) | ((KHV * h) >> 2);
         const uint32_t *sz = (const uint32_t *)(sl + XS + WS + 256 * wave);
-        o.sc = f16_to_f32(sz[si]);
-        o.zs = -(f16_to_f32(sz[32 + si]) * o.sc);
+        const float sv = f16_to_f32(sz[si]);
+        o.zs = -(f16_to_f32(sz[32 + si]) * sv);
+        o.sc = sv * kTwo24;                 // s 2^24 (dq_pair_u4)
     };
     // w = round_16(fmaf(q, s, -z s)), then the block's MFMAs
     v4f acc[MT];
@@ -736,14 +765,10 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
         XV wfs[4 * KHV];
 #pragma unroll
         for (int t = 0; t < 4 * KHV; t++) {
-            const uint32_t p = (uint32_t)o.wv[t >> 2][t & 3];
-            const uint32_t lo = p & 0x0f0f0f0fu, hi = (p >> 4) & 0x0f0f0f0fu;   // even / odd k
-            float q0[4], q1[4];
-            ubytes_to_f32(lo, q0);
-            ubytes_to_f32(hi, q1);
+            const Nib4 v = nib_split((uint32_t)o.wv[t >> 2][t & 3]);
             uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) w[e] = pack2<XDT>(__builtin_fmaf(q0[e], o.sc, o.zs), __builtin_fmaf(q1[e], o.sc, o.zs));
+            for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.zs);
             wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
         }
 #pragma unroll
@@ -892,22 +917,19 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
         }
         const int si = (nr << 1) | (h >> 1);
         const uint32_t *sz = (const uint32_t *)(sl + WBYTES);
-        o.sc = f16_to_f32(sz[si]);
-        o.zs = -(f16_to_f32(sz[32 + si]) * o.sc);
+        const float sv = f16_to_f32(sz[si]);
+        o.zs = -(f16_to_f32(sz[32 + si]) * sv);
+        o.sc = sv * kTwo24;                 // s 2^24 (dq_pair_u4)
     };
     v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](const Ops &o) {
         XV wfs[8];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            const uint32_t p = (uint32_t)o.wv[t >> 2][t & 3];
-            const uint32_t lo = p & 0x0f0f0f0fu, hi = (p >> 4) & 0x0f0f0f0fu;   // even / odd k
-            float q0[4], q1[4];
-            ubytes_to_f32(lo, q0);
-            ubytes_to_f32(hi, q1);
+            const Nib4 v = nib_split((uint32_t)o.wv[t >> 2][t & 3]);
             uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) w[e] = pack2<XDT>(__builtin_fmaf(q0[e], o.sc, o.zs), __builtin_fmaf(q1[e], o.sc, o.zs));
+            for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.zs);
             wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
         }
 #pragma unroll
