@@ -1046,10 +1046,13 @@ constexpr int64_t SKINNY_MAX_M = 64;   // largest M of the streaming and skinny 
 
 // Split-K reduction: y = round_out(fmaf(((p_0 + p_1) + ...) + p_{S-1}, cs[n], bias[n])) over the
 // partial tiles of the tiled kernel (cs = the int8 row scale, 1 for uint4), the tiled kernel's
-// epilogue on the sum taken in split order.  One thread per 4 consecutive columns of a row.
+// epilogue on the sum taken in split order.  One thread per 4 consecutive columns of a row; when
+// the row and the bias are aligned for it, the 4 outputs go out as one 8-byte (16-bit outputs) or
+// 16-byte (fp32) store and the bias comes in as one word (per-element 2-byte stores and loads made
+// the reduction of M=128 x N=25600, 33 MB of partials and outputs, take 9.4 us).
 template <int BM>
 __global__ void __launch_bounds__(256)
-wonly_splitk_reduce(const float *__restrict__ part, int S, int M, int N, WArgs wa)
+wonly_splitk_reduce(const float *__restrict__ part, int S, int M, int N, WArgs wa, int vec)
 {
     const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int nq = (N + 3) / 4;
@@ -1063,7 +1066,36 @@ wonly_splitk_reduce(const float *__restrict__ part, int S, int M, int N, WArgs w
         const v4f u = *(const v4f *)(p + (int64_t)sp * (BM * wt::BN));
         t = v4f{t[0] + u[0], t[1] + u[1], t[2] + u[2], t[3] + u[3]};
     }
-    uint8_t *row = (uint8_t *)wa.y + (int64_t)m * wa.ldy * (wa.y_dtype == PSQ_F32 ? 4 : 2);
+    const int64_t ysz = wa.y_dtype == PSQ_F32 ? 4 : 2;
+    uint8_t *row = (uint8_t *)wa.y + (int64_t)m * wa.ldy * ysz;
+    if (vec && n + 3 < N) {
+        float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (wa.bias) {
+            if (wa.bias_dtype == PSQ_F32) {
+                const v4f bv = *(const v4f *)((const float *)wa.bias + n);
+                b[0] = bv[0]; b[1] = bv[1]; b[2] = bv[2]; b[3] = bv[3];
+            } else {
+                const v2i bv = *(const v2i *)((const uint16_t *)wa.bias + n);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t w = (uint32_t)bv[c >> 1], h16 = (c & 1) ? w >> 16 : w & 0xffffu;
+                    b[c] = wa.bias_dtype == PSQ_BF16 ? bf16_to_f32(h16) : f16_to_f32(h16);
+                }
+            }
+        }
+        float o[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) o[c] = __builtin_fmaf(t[c], wa.scale32 ? wa.scale32[n + c] : 1.0f, b[c]);
+        if (wa.y_dtype == PSQ_F32) {
+            *(v4f *)(row + (int64_t)n * 4) = v4f{o[0], o[1], o[2], o[3]};
+        } else {
+            uint32_t h[4];     // the rounding of store_elem
+#pragma unroll
+            for (int c = 0; c < 4; c++) h[c] = wa.y_dtype == PSQ_BF16 ? f32_to_bf16(o[c]) : f32_to_f16(o[c]);
+            *(v2i *)(row + (int64_t)n * 2) = v2i{(int)(h[0] | (h[1] << 16)), (int)(h[2] | (h[3] << 16))};
+        }
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         if (n + c >= N) break;
@@ -1091,9 +1123,13 @@ int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_
     kern<<<dim3((unsigned)(tiles * wa.ksplit)), dim3(wt::THREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
     if (wa.ksplit > 1) {
         if (int e = check_launch(name)) return e;
-        const int64_t threads = M * ((N + 3) / 4);
-        wonly_splitk_reduce<BM><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st>>>(wa.part, wa.ksplit,
-                                                                                             (int)M, (int)N, wa);
+        // whole-quad stores and bias words: 8-byte aligned rows (16-byte for fp32) and bias
+        const int64_t ysz = wa.y_dtype == PSQ_F32 ? 4 : 2, bsz = wa.bias_dtype == PSQ_F32 ? 4 : 2;
+        const int vec = ((uintptr_t)wa.y % (4 * ysz) == 0 && (wa.ldy * ysz) % (4 * ysz) == 0 &&
+                         (!wa.bias || (uintptr_t)wa.bias % (4 * bsz) == 0)) ? 1 : 0;
+        const int64_t quads = M * ((N + 3) / 4);
+        wonly_splitk_reduce<BM><<<dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st>>>(wa.part, wa.ksplit, (int)M,
+                                                                                           (int)N, wa, vec);
     }
     return check_launch(name);
 }
