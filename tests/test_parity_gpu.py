@@ -327,6 +327,51 @@ def test_gemm_w8a16_split_k(gpu, M, N, K):
     assert_fp32_path(y32.cpu()[rows], yb.cpu()[rows], ref, f"w8a16 split-K {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("out_dt,bias_dt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                            (torch.float32, torch.float32)])
+def test_gemm_w4a16_split_k_output_layouts(gpu, out_dt, bias_dt):
+    """The split-K reduction writes a thread's 4 columns with one store and reads their bias as one
+    word when the rows and the bias allow it, element by element otherwise.  Every layout gives the
+    same bits: padded rows (aligned, N not a multiple of 4: a partial last quad), odd row strides,
+    a bias that starts at an odd element."""
+    import ctypes
+    from powershard_amd import _native
+    M, N, K, gs = 128, 2050, 2048, 128
+    assert _split_plan(M, N, K, gs) > 0, "shape expected to split"
+    x = heavy_rows(M, K, seed=100, outlier_frac=0).to(gpu)
+    w = torch.randn(N, K, generator=seeded(101)) * 0.02
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    wq, s, z = wq.to(gpu), s.to(gpu), z.to(gpu)
+    bias_store = (torch.randn(N + 1, generator=seeded(102)) * 0.01).to(bias_dt).to(gpu)
+    lib = _native.lib()
+    nb = lib.psq_gemm_wonly_workspace_bytes(_native.W_UINT4, K, M, N, K, gs)
+    ws = torch.empty(nb, dtype=torch.uint8, device=gpu)
+    st = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    code = {torch.bfloat16: _native.BF16, torch.float16: _native.F16, torch.float32: _native.F32}
+
+    def run(ldy, bias):
+        y = torch.full((M, ldy), float("nan"), dtype=out_dt, device=gpu)
+        rc = lib.psq_gemm_w4a16_ws(P(x), _native.BF16, K, P(wq), P(s), P(z), gs, P(bias), code[bias_dt], P(y),
+                                   code[out_dt], ldy, M, N, K, P(ws), nb, st)
+        assert rc == 0, _native.last_error()
+        torch.cuda.synchronize()
+        return y[:, :N].cpu()
+
+    bits = lambda t: t.view(torch.uint8)
+    aligned = run(N + 2, bias_store[:N])           # padded rows: whole-quad stores, scalar last quad
+    for ldy in (N, N + 1):                         # rows not aligned for whole-quad stores
+        assert torch.equal(bits(aligned), bits(run(ldy, bias_store[:N]))), f"ldy={ldy}: outputs differ"
+    shifted = bias_store[1:]                       # starts at an odd element: read element by element
+    assert torch.equal(bits(run(N + 2, shifted)), bits(run(N + 2, shifted.clone()))), "odd bias offset"
+    wd = oracle.dequant_uint4(wq.cpu(), s.cpu(), z.cpu(), gs)
+    rows = _sample_rows(M, 32, 103)
+    ref = _wonly_rows(x.cpu(), wd, bias_store[:N].cpu(), rows).float()
+    err = (aligned[rows].float() - ref).abs()
+    bar = torch.maximum(torch.full_like(ref, 1e-2 * ref.pow(2).mean().sqrt().item()), ref.abs() * 2.0 ** -7)
+    assert torch.all(err <= bar), f"max err {err.max().item()}"
+
+
 def test_gemm_w4a16_unsplit_entry_point(gpu):
     """psq_gemm_w4a16 (no workspace) keeps the unsplit kernel; its output meets the same bar."""
     import ctypes
