@@ -74,7 +74,8 @@ __device__ __forceinline__ void ubytes_to_f32(uint32_t w, float (&f)[4])
 // fp16 subnormal q * 2^-24, and v_fma_mix_f32 takes an fp16 operand as is, so
 //   fma_mix(q * 2^-24, s * 2^24, c) = fmaf(q, s, c)
 // exactly: s * 2^24 is an exact fp32 scaling of the fp16 scale and the fma's product is exact
-// (checked on gfx950 for all q against fmaf over 2^20 fp16 scales, subnormal ones included).
+// (tests/test_parity_gpu.py::test_w4a16_dequantized_weights_exact checks every kernel's weights
+// bit for bit against round_16(fmaf(q, s, -z s)), fp16-subnormal scales included).
 // The eight nibbles of a word (nibble i = k offset i) are split into four such pairs with 7 ops,
 // then one fma_mix per weight: 19 VALU ops per 8 weights with the packs, against 23 for
 // v_cvt_f32_ubyte + v_fma_f32.

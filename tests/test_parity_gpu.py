@@ -327,6 +327,38 @@ def test_gemm_w8a16_split_k(gpu, M, N, K):
     assert_fp32_path(y32.cpu()[rows], yb.cpu()[rows], ref, f"w8a16 split-K {M}x{N}x{K}")
 
 
+def _fma_form_weights(wq, s, z, gs, cols, dtype):
+    """round_16(fmaf(q, s, -z s)) of weight columns `cols`, as float32 [N, len(cols)]: the per-weight
+    arithmetic of the decode, streaming and tiled uint4 kernels.  fmaf is exact in float64 here (q s
+    has at most 15 significant bits, -z s is the fp32 product rounded once), then rounded once to
+    fp32 and once to the 16-bit type."""
+    k = cols.long()
+    q = ((wq[:, k // 2].int() >> (4 * (k % 2)).int()) & 15).double()
+    sg, zg = s[:, k // gs].float(), z[:, k // gs].float()
+    c = -(zg * sg)                                        # fp32 product, rounded once
+    return (q * sg.double() + c.double()).float().to(dtype).float()
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [4, 48, 160])      # decode, streaming, tiled (split-K) kernels
+def test_w4a16_dequantized_weights_exact(gpu, M, xdt):
+    """One-hot activation rows make every output one dequantized weight (the MFMA adds zeros to a
+    single product), so each kernel's uint4 dequantization -- the nibble as an fp16 subnormal into
+    v_fma_mix_f32 -- is checked bit for bit against round_16(fmaf(q, s, -z s))."""
+    from powershard_amd import ops
+    K, N, gs = 1024, 640, 128
+    w = torch.randn(N, K, generator=seeded(110)) * 0.02
+    w[:, :128] *= 1e-3                                    # tiny scales (fp16 subnormal range) in group 0
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    cols = (torch.arange(M) * 37 + 5) % K                 # spread over every group and nibble position
+    x = torch.zeros(M, K, dtype=xdt)
+    x[torch.arange(M), cols] = 1
+    y = ops.gemm_w4a16(x.to(gpu), wq.to(gpu), s.to(gpu), z.to(gpu), gs, None, out_dtype=torch.float32).cpu()
+    want = _fma_form_weights(wq, s, z, gs, cols, xdt).T
+    bad = (y != want).sum().item()
+    assert bad == 0, f"{bad} of {y.numel()} dequantized weights differ"
+
+
 @pytest.mark.parametrize("out_dt,bias_dt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                             (torch.float32, torch.float32)])
 def test_gemm_w4a16_split_k_output_layouts(gpu, out_dt, bias_dt):
