@@ -37,11 +37,13 @@ struct WArgs {
     void *y;
     int y_dtype;
     int64_t ldy;
-    // split-K of the tiled kernel (ksplit > 1): per output tile, ksplit workgroups take
-    // contiguous ranges of its K stages and write their fp32 partial tiles to `part`; a second
-    // kernel adds them in split order and applies the epilogue
-    int ksplit = 1;
-    float *part = nullptr;      // [tile row][tile column][ksplit][BM][256] fp32
+    // stream-K of the tiled kernel (sk > 0): the (tile, K stage) units of all tiles, tile after
+    // tile, are cut into sk equal contiguous ranges, one per workgroup; a workgroup whose range
+    // holds part of a tile's stages writes its fp32 partial tile to `part`, and the last of the
+    // tile's workgroups to finish adds the partials in K order and applies the epilogue
+    int sk = 0;
+    float *part = nullptr;      // [2 sk][BM][256] fp32: the first and the last partial of each workgroup
+    uint32_t *cnt = nullptr;    // [tiles] finished workgroups per tile, zero at launch
 };
 
 template <int XDT>
@@ -278,9 +280,19 @@ template <int WK, int BM> constexpr int lds_bytes()
 // activation chunk swizzle: bijective on 8 consecutive rows (32 banks) and on each parity class
 // of 16 consecutive rows (64 banks), so a fragment read (32 rows, one logical chunk) is conflict free
 __device__ __forceinline__ int xsw(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
+// Stream-K over U units and G workgroup ranges, range l = [floor(l U / G), floor((l + 1) U / G)):
+// the range holding unit u (the largest l with floor(l U / G) <= u; ranges are never empty when
+// U >= G) ...
+__host__ __device__ inline int sk_owner(int64_t u, int64_t U, int G) { return (int)(((u + 1) * G + U - 1) / U) - 1; }
+// ... and the partial-tile slot of range l's segment of tile t: 2 l for the range's first tile,
+// 2 l + 1 for its last (a range's other tiles are whole and need none)
+__host__ __device__ inline int sk_slot(int l, int t, int64_t U, int G, int nk)
+{
+    return 2 * l + (t == (int)((int64_t)l * U / G / nk) ? 0 : 1);
+}
 }  // namespace wt
 
-template <int XDT, int WK, int BM>
+template <int XDT, int WK, int BM, bool SKM>
 __global__ void __launch_bounds__(wt::THREADS, 1)
 gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
 {
@@ -299,325 +311,415 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int frow = lane & 31, h = lane >> 5;
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
-    const int S = wa.ksplit;                                 // workgroups per tile (split-K)
-    const int tile = (int)(blockIdx.x / (unsigned)S), split = (int)blockIdx.x - tile * S;
-    int pm, pn;
-    tile_order(tile, nbm, nbn, 4, pm, pn);
-    const int m0 = pm * BM, n0 = pn * BN;
-    // this workgroup's K stages [kb, kb + nk) of the tile (all of them without a split)
     const int nk_all = K / BK;
-    const int kb = (int)((int64_t)split * nk_all / S);
-    const int nk = (int)((int64_t)(split + 1) * nk_all / S) - kb;
     const int G = WK == W_UINT4 ? K / wa.gs : 1;
     const int64_t wld = WK == W_UINT4 ? K / 2 : K;          // weight row bytes
-
-    // ---- ring loads (scalar base + 32-bit lane offsets); rows past M / N clamp to the last row
-    uint32_t xo[XDMA], wo[WDMA];
-#pragma unroll
-    for (int j = 0; j < XDMA; j++) {
-        const int b = j * NWAVE + wave, r = 8 * b + (lane >> 3);
-        const int c = (lane & 7) ^ xsw(r);
-        xo[j] = (uint32_t)(min(r, M - 1 - m0) * ldx * 2 + c * 16);
-    }
-#pragma unroll
-    for (int j = 0; j < WDMA; j++) {
-        const int b = j * NWAVE + wave;
-        const int per = 1024 / RB;                          // rows per load (32 / 16)
-        const int r = per * b + lane / (64 / per);
-        wo[j] = (uint32_t)(min(r, N - 1 - n0) * wld + (lane % (64 / per)) * 16);
-    }
-    const int scol = min(n0 + 64 * (wave & 3) + lane, N - 1);   // scale (waves 0-3) / zero (4-7) column of this lane
-    const unsigned spg = WK == W_UINT4 ? (unsigned)(wa.gs / BK) : 1u;   // stages per group
-    // Scale / zero blocks (uint4, groups per row a multiple of SZG, 16-byte aligned tables): a
-    // block of SZG groups is loaded once, with the first stage of the block (or of the workgroup's
-    // K range), instead of a 2-byte scattered load per stage.  Otherwise the per-stage loads.
-    // (stages per group a power of two, so that a stage's group and block are shifts and masks:
-    // the per-stage bookkeeping sits between the MFMAs)
-    const bool szblk = WK == W_UINT4 && G % SZG == 0 && (spg & (spg - 1)) == 0 && ((uintptr_t)wa.scale16 % 16) == 0 &&
-                       ((uintptr_t)wa.zero16 % 16) == 0;
-    const int spg_sh = spg ? __builtin_ctz(spg) : 0;          // log2 stages per group (szblk)
-    static_assert(SZG == 8, "scale blocks of 8 groups");
-    const unsigned spb_mask = (spg << 3) - 1;                 // stages per scale block - 1
-    uint8_t *const szbuf = smem + NSTAGE * SLOT;
-    const uint8_t *xb = (const uint8_t *)(x + (int64_t)m0 * ldx);
-    const uint8_t *wb = wa.wq + (int64_t)n0 * wld;
-    // The tile's activation and weight rows as buffer descriptors: a load is the descriptor, the
-    // stage's k offset as scalar offset and the lane's row offset as vector offset (no per-load
-    // address arithmetic).
-    const __amdgpu_buffer_rsrc_t rsx = raw_rsrc(xb), rsw = raw_rsrc(wb);
-    // load q of a stage (q < 8: activation block q; then weight blocks; then, for uint4, the
-    // stage's scale and zero words of the wave's 64 columns)
-    auto issue_one = [&](int slot, int kt, auto qc) {
-        constexpr int q = decltype(qc)::value;
-        uint8_t *sl = smem + slot * SLOT;
-        if constexpr (q < XDMA) {
-            constexpr int b8 = q * NWAVE;
-            buffer_load_lds16(rsx, (lds_ptr)(sl + 1024 * (b8 + wave)), xo[q], kt * BK * 2);
-        } else if constexpr (q < XDMA + WDMA) {
-            constexpr int j = q - XDMA;
-            buffer_load_lds16(rsw, (lds_ptr)(sl + XBYTES + 1024 * (j * NWAVE + wave)), wo[j], kt * RB);
-        } else if constexpr (WK == W_UINT4) {
-            const bool zero = wave >= 4;
-            if (szblk) {
-                // the block of the stage's group, with the block's first stage (or the range's)
-                if (kt == kb || ((unsigned)kt & spb_mask) == 0) {
-                    const unsigned blk = (unsigned)kt >> (spg_sh + 3);
-                    const int64_t gi = (int64_t)scol * G + SZG * blk;
-                    __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
-                                                     (lds_ptr)(szbuf + (blk & 1) * SZB_BYTES + 1024 * wave), 16, 0, 0);
-                }
-            } else {
-                const int64_t gi = (int64_t)scol * G + (int)((unsigned)kt / spg);   // the stage's group
-                __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
-                                                 (lds_ptr)(sl + XBYTES + BN * RB + 256 * wave), 2, 0, 0);
-            }
-        }
-    };
-    auto issue_all = [&](int slot, int kt) {
-        [&]<int... Q>(std::integer_sequence<int, Q...>) {
-            (issue_one(slot, kt, std::integral_constant<int, Q>{}), ...);
-        }(std::make_integer_sequence<int, LPS>{});
-    };
-
-    // ---- fragments
-    auto read_x = [&](int slot, int t, int i) -> XV {
-        const int r = 32 * i + frow, c = 4 * h + t;
-        return __builtin_bit_cast(XV, *(const v4i *)(smem + slot * SLOT + r * XROW + ((c ^ xsw(r)) << 4)));
-    };
-    // the lane's packed weights of a stage (its 32 k of each of its two columns) and, for uint4,
-    // the columns' group scale s (held as s 2^24) and -z s: a weight is round_16(fmaf(q, s, -z s)),
-    // one fma_mix per weight (dq_pair_u4)
-    struct WRaw { v4i w[TN][RB / 32]; float s[TN], z[TN]; };
-    auto read_w = [&](int slot, int kt, WRaw &r) {
-        const uint8_t *sl = smem + slot * SLOT + XBYTES;
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = WCOLS * wave + 32 * j + frow;
-#pragma unroll
-            for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
-            if constexpr (WK == W_UINT4) {
-                float sv, zv;
-                if (szblk) {
-                    const unsigned g = (unsigned)kt >> spg_sh;
-                    const uint8_t *zb = szbuf + ((g / SZG) & 1) * SZB_BYTES + 16 * n + 2 * (g % SZG);
-                    sv = f16_to_f32(*(const uint16_t *)zb);
-                    zv = f16_to_f32(*(const uint16_t *)(zb + BN * 16));
-                } else {
-                    sv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
-                    zv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n));
-                }
-                r.s[j] = sv * kTwo24;     // s 2^24 for the fp16-subnormal nibbles (dq_pair_u4)
-                r.z[j] = -(zv * sv);      // -z s
-            } else {
-                r.s[j] = 1.0f;
-                r.z[j] = 0.0f;
-            }
-        }
-    };
-    // pair e (k = 32 h + 8 t + 2e, +1) of column tile j's weights in k-step t, packed
-    auto dq_pair = [&](const WRaw &r, int j, int t, int e) -> uint32_t {
-        if constexpr (WK == W_UINT4) {
-            return dq_pair_u4<XDT>(nib_split((uint32_t)r.w[j][0][t]), e, r.s[j], r.z[j]);
-        } else {
-            const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
-            const int sh = 16 * (e & 1);
-            return pack2<XDT>((float)(int8_t)((p >> sh) & 0xffu), (float)(int8_t)((p >> (sh + 8)) & 0xffu));
-        }
-    };
-
-    v16f acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-    auto mfma = [&](int i, int j, const XV &wf, const XV &xf) {
-        if constexpr (XDT == PSQ_BF16)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf, acc[i][j], 0, 0, 0);
-        else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, xf, acc[i][j], 0, 0, 0);
-    };
-
-    // Stage kt + 1 landed: every load but those of the NSTAGE - 2 younger stages is complete.  With
-    // scale blocks a stage issues LPS - 1 loads plus, at a block start, the block's: counting only
-    // the LPS - 1 waits for at least the loads it must (the block's is older than the younger
-    // stages' loads).
-    auto wait_stage = [&] {
-        if constexpr (WK == W_UINT4) {
-            if (szblk) wait_vmcnt<(NSTAGE - 2) * (LPS - 1)>();
-            else wait_vmcnt<(NSTAGE - 2) * LPS>();
-        } else {
-            wait_vmcnt<(NSTAGE - 2) * LPS>();
-        }
-    };
-
-    // ---- prologue: stages 0 .. NSTAGE-2 in flight, stage 0 landed, its first fragments ready
-#pragma unroll
-    for (int st = 0; st < NSTAGE - 1; st++) issue_all(st, kb + min(st, nk - 1));
-    wait_stage();
-    stage_barrier();
-    WRaw wr;
-    read_w(0, kb, wr);
-    XV xa[TM], xb2[TM], wa0[TN], wb0[TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++) xa[i] = read_x(0, 0, i);
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-        uint32_t hw[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) hw[e] = dq_pair(wr, j, 0, e);
-        wa0[j] = __builtin_bit_cast(XV, v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]});
-    }
-
-    // One k-step: the NQ = TM TN MFMAs of step t on (xc, wc); behind MFMA q the activation
-    // fragment q / TN of the next step (q % TN == 0), one of the next step's 4 TN weight pairs
-    // (every NQ / (4 TN)-th MFMA), and for k-steps 0-2 a third of the stage's refill loads.
-    // The instruction order is pinned: sched_barrier after every MFMA.
-    auto kstep = [&](auto tnc, auto basec, XV (&xc)[TM], XV (&wc)[TN], XV (&xn)[TM], XV (&wn)[TN], int xslot,
-                     const WRaw &wraw, int fill_slot, int fill_kt) {
-        constexpr int tn = decltype(tnc)::value, fill_base = decltype(basec)::value;
-        uint32_t hw[TN][4];
-        [&]<int... Q>(std::integer_sequence<int, Q...>) {
-            ([&] {
-                constexpr int q = Q;
-                mfma(q / TN, q % TN, wc[q % TN], xc[q / TN]);
-                if constexpr (q % TN == 0) xn[q / TN] = read_x(xslot, tn, q / TN);
-                // weight pair pi (column tile pi / 4, pair pi % 4), spread evenly over the k-step
-                constexpr int NP = 4 * TN, PSTRIDE = NQ / NP;
-                static_assert(NQ % NP == 0, "pairs per k-step must divide the MFMAs");
-                constexpr int pi = q % PSTRIDE == 0 ? q / PSTRIDE : -1;
-                if constexpr (pi >= 0) hw[pi >> 2][pi & 3] = dq_pair(wraw, pi >> 2, tn, pi & 3);
-                // the refill loads: LPK of them spread over the k-step, the last of each group
-                constexpr int per = NQ / LPK, u = q / per;
-                if constexpr (fill_base >= 0 && q % per == per - 1 && u < LPK && fill_base + u < LPS)
-                    issue_one(fill_slot, fill_kt, std::integral_constant<int, fill_base + u>{});
-                __builtin_amdgcn_sched_barrier(0);
-            }(), ...);
-        }(std::make_integer_sequence<int, NQ>{});
-#pragma unroll
-        for (int j = 0; j < TN; j++) wn[j] = __builtin_bit_cast(XV, v4i{(int)hw[j][0], (int)hw[j][1], (int)hw[j][2], (int)hw[j][3]});
-    };
-    int rs = 0;
+    // Stream-K: the workgroup's units [u0, u1) (unit = (tile, K stage); tile-major, the tiles of a
+    // column of tiles, which share their weights, consecutive), taken as segments of one tile
+    // each, from the last to the first.  A range's first segment is the end of a tile that other
+    // workgroups began earlier in their runs, so the workgroup that finishes a tile, and adds it
+    // up, is most often the one that holds that segment.  Without stream-K one segment: every
+    // stage of tile blockIdx.x.
+    const int SK = SKM ? wa.sk : 0;
+    const int64_t U = (int64_t)nbm * nbn * nk_all;
+    const int lw = SK ? xcd_rank((int)blockIdx.x, SK) : 0;   // consecutive ranges on one XCD
+    const int64_t u0 = SK ? (int64_t)lw * U / SK : 0;
+    int64_t ue = SK ? (int64_t)(lw + 1) * U / SK : nk_all;
+    bool first_seg = true;
 #pragma clang loop unroll(disable)
-    for (int kt = 0; kt < nk; kt++) {
-        const int fill = rs == 0 ? NSTAGE - 1 : rs - 1;     // ring slot of stage kt + NSTAGE - 1
-        const int kfill = kb + min(kt + NSTAGE - 1, nk - 1); // (past the end: re-load the last stage)
-        const int nxt = rs == NSTAGE - 1 ? 0 : rs + 1;
-        using I = std::integral_constant<int, 0>;
-        kstep(std::integral_constant<int, 1>{}, I{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
-        kstep(std::integral_constant<int, 2>{}, std::integral_constant<int, LPK>{}, xb2, wb0, xa, wa0, rs, wr, fill, kfill);
-        kstep(std::integral_constant<int, 3>{}, std::integral_constant<int, 2 * LPK>{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
-        // stage kt + 1 landed for every wave; nobody reads stage kt's slot any more
+    while (ue > u0) {
+        int tile, kb, nk, pm, pn;   // this segment: K stages [kb, kb + nk) of tile (pm, pn)
+        if (SK) {
+            tile = (int)((ue - 1) / nk_all);
+            const int64_t tb = (int64_t)tile * nk_all;
+            kb = (int)((u0 > tb ? u0 : tb) - tb);
+            nk = (int)(ue - tb) - kb;
+            ue = tb + kb;
+            pm = tile % nbm;
+            pn = tile / nbm;
+        } else {
+            tile = (int)blockIdx.x;
+            kb = 0;
+            nk = nk_all;
+            ue = 0;
+            tile_order(tile, nbm, nbn, 4, pm, pn);
+        }
+        // every wave is done with the previous segment's ring and scale blocks before the refill
+        if (!first_seg) __syncthreads();
+        first_seg = false;
+        const int m0 = pm * BM, n0 = pn * BN;
+
+        // ---- ring loads (scalar base + 32-bit lane offsets); rows past M / N clamp to the last row
+        uint32_t xo[XDMA], wo[WDMA];
+#pragma unroll
+        for (int j = 0; j < XDMA; j++) {
+            const int b = j * NWAVE + wave, r = 8 * b + (lane >> 3);
+            const int c = (lane & 7) ^ xsw(r);
+            xo[j] = (uint32_t)(min(r, M - 1 - m0) * ldx * 2 + c * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < WDMA; j++) {
+            const int b = j * NWAVE + wave;
+            const int per = 1024 / RB;                          // rows per load (32 / 16)
+            const int r = per * b + lane / (64 / per);
+            wo[j] = (uint32_t)(min(r, N - 1 - n0) * wld + (lane % (64 / per)) * 16);
+        }
+        const int scol = min(n0 + 64 * (wave & 3) + lane, N - 1);   // scale (waves 0-3) / zero (4-7) column of this lane
+        const unsigned spg = WK == W_UINT4 ? (unsigned)(wa.gs / BK) : 1u;   // stages per group
+        // Scale / zero blocks (uint4, groups per row a multiple of SZG, 16-byte aligned tables): a
+        // block of SZG groups is loaded once, with the first stage of the block (or of the workgroup's
+        // K range), instead of a 2-byte scattered load per stage.  Otherwise the per-stage loads.
+        // (stages per group a power of two, so that a stage's group and block are shifts and masks:
+        // the per-stage bookkeeping sits between the MFMAs)
+        const bool szblk = WK == W_UINT4 && G % SZG == 0 && (spg & (spg - 1)) == 0 && ((uintptr_t)wa.scale16 % 16) == 0 &&
+                           ((uintptr_t)wa.zero16 % 16) == 0;
+        const int spg_sh = spg ? __builtin_ctz(spg) : 0;          // log2 stages per group (szblk)
+        static_assert(SZG == 8, "scale blocks of 8 groups");
+        const unsigned spb_mask = (spg << 3) - 1;                 // stages per scale block - 1
+        uint8_t *const szbuf = smem + NSTAGE * SLOT;
+        const uint8_t *xb = (const uint8_t *)(x + (int64_t)m0 * ldx);
+        const uint8_t *wb = wa.wq + (int64_t)n0 * wld;
+        // The tile's activation and weight rows as buffer descriptors: a load is the descriptor, the
+        // stage's k offset as scalar offset and the lane's row offset as vector offset (no per-load
+        // address arithmetic).
+        const __amdgpu_buffer_rsrc_t rsx = raw_rsrc(xb), rsw = raw_rsrc(wb);
+        // load q of a stage (q < 8: activation block q; then weight blocks; then, for uint4, the
+        // stage's scale and zero words of the wave's 64 columns)
+        auto issue_one = [&](int slot, int kt, auto qc) {
+            constexpr int q = decltype(qc)::value;
+            uint8_t *sl = smem + slot * SLOT;
+            if constexpr (q < XDMA) {
+                constexpr int b8 = q * NWAVE;
+                buffer_load_lds16(rsx, (lds_ptr)(sl + 1024 * (b8 + wave)), xo[q], kt * BK * 2);
+            } else if constexpr (q < XDMA + WDMA) {
+                constexpr int j = q - XDMA;
+                buffer_load_lds16(rsw, (lds_ptr)(sl + XBYTES + 1024 * (j * NWAVE + wave)), wo[j], kt * RB);
+            } else if constexpr (WK == W_UINT4) {
+                const bool zero = wave >= 4;
+                if (szblk) {
+                    // the block of the stage's group, with the block's first stage (or the range's)
+                    if (kt == kb || ((unsigned)kt & spb_mask) == 0) {
+                        const unsigned blk = (unsigned)kt >> (spg_sh + 3);
+                        const int64_t gi = (int64_t)scol * G + SZG * blk;
+                        __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
+                                                         (lds_ptr)(szbuf + (blk & 1) * SZB_BYTES + 1024 * wave), 16, 0, 0);
+                    }
+                } else {
+                    const int64_t gi = (int64_t)scol * G + (int)((unsigned)kt / spg);   // the stage's group
+                    __builtin_amdgcn_global_load_lds((glb_ptr)((zero ? wa.zero16 : wa.scale16) + gi),
+                                                     (lds_ptr)(sl + XBYTES + BN * RB + 256 * wave), 2, 0, 0);
+                }
+            }
+        };
+        auto issue_all = [&](int slot, int kt) {
+            [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                (issue_one(slot, kt, std::integral_constant<int, Q>{}), ...);
+            }(std::make_integer_sequence<int, LPS>{});
+        };
+
+        // ---- fragments
+        auto read_x = [&](int slot, int t, int i) -> XV {
+            const int r = 32 * i + frow, c = 4 * h + t;
+            return __builtin_bit_cast(XV, *(const v4i *)(smem + slot * SLOT + r * XROW + ((c ^ xsw(r)) << 4)));
+        };
+        // the lane's packed weights of a stage (its 32 k of each of its two columns) and, for uint4,
+        // the columns' group scale s (held as s 2^24) and -z s: a weight is round_16(fmaf(q, s, -z s)),
+        // one fma_mix per weight (dq_pair_u4)
+        struct WRaw { v4i w[TN][RB / 32]; float s[TN], z[TN]; };
+        auto read_w = [&](int slot, int kt, WRaw &r) {
+            const uint8_t *sl = smem + slot * SLOT + XBYTES;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = WCOLS * wave + 32 * j + frow;
+#pragma unroll
+                for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
+                if constexpr (WK == W_UINT4) {
+                    float sv, zv;
+                    if (szblk) {
+                        const unsigned g = (unsigned)kt >> spg_sh;
+                        const uint8_t *zb = szbuf + ((g / SZG) & 1) * SZB_BYTES + 16 * n + 2 * (g % SZG);
+                        sv = f16_to_f32(*(const uint16_t *)zb);
+                        zv = f16_to_f32(*(const uint16_t *)(zb + BN * 16));
+                    } else {
+                        sv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
+                        zv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n));
+                    }
+                    r.s[j] = sv * kTwo24;     // s 2^24 for the fp16-subnormal nibbles (dq_pair_u4)
+                    r.z[j] = -(zv * sv);      // -z s
+                } else {
+                    r.s[j] = 1.0f;
+                    r.z[j] = 0.0f;
+                }
+            }
+        };
+        // pair e (k = 32 h + 8 t + 2e, +1) of column tile j's weights in k-step t, packed
+        auto dq_pair = [&](const WRaw &r, int j, int t, int e) -> uint32_t {
+            if constexpr (WK == W_UINT4) {
+                return dq_pair_u4<XDT>(nib_split((uint32_t)r.w[j][0][t]), e, r.s[j], r.z[j]);
+            } else {
+                const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
+                const int sh = 16 * (e & 1);
+                return pack2<XDT>((float)(int8_t)((p >> sh) & 0xffu), (float)(int8_t)((p >> (sh + 8)) & 0xffu));
+            }
+        };
+
+        v16f acc[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+        auto mfma = [&](int i, int j, const XV &wf, const XV &xf) {
+            if constexpr (XDT == PSQ_BF16)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf, acc[i][j], 0, 0, 0);
+            else
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, xf, acc[i][j], 0, 0, 0);
+        };
+
+        // Stage kt + 1 landed: every load but those of the NSTAGE - 2 younger stages is complete.  With
+        // scale blocks a stage issues LPS - 1 loads plus, at a block start, the block's: counting only
+        // the LPS - 1 waits for at least the loads it must (the block's is older than the younger
+        // stages' loads).
+        auto wait_stage = [&] {
+            if constexpr (WK == W_UINT4) {
+                if (szblk) wait_vmcnt<(NSTAGE - 2) * (LPS - 1)>();
+                else wait_vmcnt<(NSTAGE - 2) * LPS>();
+            } else {
+                wait_vmcnt<(NSTAGE - 2) * LPS>();
+            }
+        };
+
+        // ---- prologue: stages 0 .. NSTAGE-2 in flight, stage 0 landed, its first fragments ready
+#pragma unroll
+        for (int st = 0; st < NSTAGE - 1; st++) issue_all(st, kb + min(st, nk - 1));
         wait_stage();
         stage_barrier();
-        read_w(nxt, kb + kt + 1, wr);
-        kstep(I{}, std::integral_constant<int, -1>{}, xb2, wb0, xa, wa0, nxt, wr, 0, 0);
-        rs = nxt;
-    }
-    wait_vmcnt<0>();   // the re-issued tail loads land before the workgroup's LDS is released
-
-    // ---- split-K (128-row tiles only): this K range's partial tile, row-major, for the reduction
-    if constexpr (BM == 128) if (S > 1) {
-        float *part = wa.part + (((int64_t)pm * nbn + pn) * S + split) * (BM * BN);
-        static_for<TM>([&](auto ic) {
-            constexpr int i = decltype(ic)::value;
-            static_for<TN>([&](auto jc) {
-                constexpr int j = decltype(jc)::value;
-                static_for<4>([&](auto gc) {
-                    constexpr int g = decltype(gc)::value;
-                    // lane (row 32 i + frow) holds columns WCOLS wave + 32 j + 8 g + 4 h + 0..3
-                    float *o = part + (32 * i + frow) * BN + WCOLS * wave + 32 * j + 8 * g + 4 * h;
-                    *(v4f *)o = v4f{__int_as_float(agpr_read(acc[i][j][4 * g])),
-                                    __int_as_float(agpr_read(acc[i][j][4 * g + 1])),
-                                    __int_as_float(agpr_read(acc[i][j][4 * g + 2])),
-                                    __int_as_float(agpr_read(acc[i][j][4 * g + 3]))};
-                });
-            });
-        });
-        return;
-    }
-
-    // ---- epilogue: acc[i][j] is the transposed 32 x 32 tile, lane (l & 31) holds output row
-    // m = m0 + 32 i + (l & 31), register 4g + c column n = n0 + WCOLS wave + 32 j + 8 g + 4 h + c.
-    //   y = round_out(fmaf(acc, s[n], bias[n]))   (s = 1 for uint4)
-    const int nl0 = WCOLS * wave + 4 * h;                    // the lane's first column in the tile
-    const int esz = wa.y_dtype == PSQ_F32 ? 4 : 2;
-    uint8_t *rowp[TM];
-    bool live[TM];
+        WRaw wr;
+        read_w(0, kb, wr);
+        XV xa[TM], xb2[TM], wa0[TN], wb0[TN];
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
-        const int m = m0 + 32 * i + frow;
-        live[i] = m < M;
-        rowp[i] = (uint8_t *)wa.y + ((int64_t)min(m, M - 1) * wa.ldy + n0 + nl0) * esz;
-    }
-    // operands of the lane's 4 columns n0 + nl0 + nc .. + 3: the row scale (int8) and the bias
-    auto operands = [&](int nc, float (&cs)[4], float (&bs)[4]) {
+        for (int i = 0; i < TM; i++) xa[i] = read_x(0, 0, i);
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int n = min(n0 + nl0 + nc + c, N - 1);
-            cs[c] = (WK == W_INT8) ? wa.scale32[n] : 1.0f;
-            bs[c] = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
+        for (int j = 0; j < TN; j++) {
+            uint32_t hw[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) hw[e] = dq_pair(wr, j, 0, e);
+            wa0[j] = __builtin_bit_cast(XV, v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]});
         }
-    };
-    auto value = [&](int i, int j, int r, float c, float b) {
-        return __builtin_fmaf(__int_as_float(agpr_read(acc[i][j][r])), c, b);
-    };
-    const bool fast = wa.y_dtype != PSQ_F32 && n0 + BN <= N && ((uintptr_t)wa.y & 15) == 0 && (wa.ldy * 2) % 16 == 0;
-    if (fast) {
-        // lanes l and l + 32 hold the same row: one v_permlane32_swap per word gives lane l columns
-        // 16 pr + 0..7 and lane l + 32 columns 16 pr + 8..15 of the column pair pr, one 16-byte store
-        const bool bf = wa.y_dtype == PSQ_BF16;
+
+        // One k-step: the NQ = TM TN MFMAs of step t on (xc, wc); behind MFMA q the activation
+        // fragment q / TN of the next step (q % TN == 0), one of the next step's 4 TN weight pairs
+        // (every NQ / (4 TN)-th MFMA), and for k-steps 0-2 a third of the stage's refill loads.
+        // The instruction order is pinned: sched_barrier after every MFMA.
+        auto kstep = [&](auto tnc, auto basec, XV (&xc)[TM], XV (&wc)[TN], XV (&xn)[TM], XV (&wn)[TN], int xslot,
+                         const WRaw &wraw, int fill_slot, int fill_kt) {
+            constexpr int tn = decltype(tnc)::value, fill_base = decltype(basec)::value;
+            uint32_t hw[TN][4];
+            [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                ([&] {
+                    constexpr int q = Q;
+                    mfma(q / TN, q % TN, wc[q % TN], xc[q / TN]);
+                    if constexpr (q % TN == 0) xn[q / TN] = read_x(xslot, tn, q / TN);
+                    // weight pair pi (column tile pi / 4, pair pi % 4), spread evenly over the k-step
+                    constexpr int NP = 4 * TN, PSTRIDE = NQ / NP;
+                    static_assert(NQ % NP == 0, "pairs per k-step must divide the MFMAs");
+                    constexpr int pi = q % PSTRIDE == 0 ? q / PSTRIDE : -1;
+                    if constexpr (pi >= 0) hw[pi >> 2][pi & 3] = dq_pair(wraw, pi >> 2, tn, pi & 3);
+                    // the refill loads: LPK of them spread over the k-step, the last of each group
+                    constexpr int per = NQ / LPK, u = q / per;
+                    if constexpr (fill_base >= 0 && q % per == per - 1 && u < LPK && fill_base + u < LPS)
+                        issue_one(fill_slot, fill_kt, std::integral_constant<int, fill_base + u>{});
+                    __builtin_amdgcn_sched_barrier(0);
+                }(), ...);
+            }(std::make_integer_sequence<int, NQ>{});
 #pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int pr = 0; pr < 2; pr++) {
-                const int nc = 32 * j + 16 * pr;
-                float cs[2][4], bs[2][4];
-                operands(nc, cs[0], bs[0]);
-                operands(nc + 8, cs[1], bs[1]);
-#pragma unroll
-                for (int i = 0; i < TM; i++) {
-                    uint32_t x0[2], x1[2];
-#pragma unroll
-                    for (int hh = 0; hh < 2; hh++) {
-                        uint32_t *o = hh == 0 ? x0 : x1;
-                        const int r = 8 * pr + 4 * hh;
-                        const float v0 = value(i, j, r, cs[hh][0], bs[hh][0]), v1 = value(i, j, r + 1, cs[hh][1], bs[hh][1]);
-                        const float v2 = value(i, j, r + 2, cs[hh][2], bs[hh][2]), v3 = value(i, j, r + 3, cs[hh][3], bs[hh][3]);
-                        o[0] = bf ? pack_half2<PSQ_BF16>(v0, v1) : pack_half2<PSQ_F16>(v0, v1);
-                        o[1] = bf ? pack_half2<PSQ_BF16>(v2, v3) : pack_half2<PSQ_F16>(v2, v3);
-                    }
-                    uint32_t lo[2], hi[2];
-#pragma unroll
-                    for (int d = 0; d < 2; d++) {
-                        const auto sw = __builtin_amdgcn_permlane32_swap(x0[d], x1[d], false, false);
-                        lo[d] = sw[0];
-                        hi[d] = sw[1];
-                    }
-                    uint8_t *p = rowp[i] + (nc + 4 * h) * 2;
-                    if (live[i]) *(v4i *)p = v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-    } else {
-        const int n_left0 = N - (n0 + nl0);
-        static_for<TN>([&](auto jc) {
-            static_for<4>([&](auto gc) {
-                constexpr int j = decltype(jc)::value, g = decltype(gc)::value, nc = 32 * j + 8 * g;
-                float cs[4], bs[4];
-                operands(nc, cs, bs);
+            for (int j = 0; j < TN; j++) wn[j] = __builtin_bit_cast(XV, v4i{(int)hw[j][0], (int)hw[j][1], (int)hw[j][2], (int)hw[j][3]});
+        };
+        int rs = 0;
+#pragma clang loop unroll(disable)
+        for (int kt = 0; kt < nk; kt++) {
+            const int fill = rs == 0 ? NSTAGE - 1 : rs - 1;     // ring slot of stage kt + NSTAGE - 1
+            const int kfill = kb + min(kt + NSTAGE - 1, nk - 1); // (past the end: re-load the last stage)
+            const int nxt = rs == NSTAGE - 1 ? 0 : rs + 1;
+            using I = std::integral_constant<int, 0>;
+            kstep(std::integral_constant<int, 1>{}, I{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
+            kstep(std::integral_constant<int, 2>{}, std::integral_constant<int, LPK>{}, xb2, wb0, xa, wa0, rs, wr, fill, kfill);
+            kstep(std::integral_constant<int, 3>{}, std::integral_constant<int, 2 * LPK>{}, xa, wa0, xb2, wb0, rs, wr, fill, kfill);
+            // stage kt + 1 landed for every wave; nobody reads stage kt's slot any more
+            wait_stage();
+            stage_barrier();
+            read_w(nxt, kb + kt + 1, wr);
+            kstep(I{}, std::integral_constant<int, -1>{}, xb2, wb0, xa, wa0, nxt, wr, 0, 0);
+            rs = nxt;
+        }
+        wait_vmcnt<0>();   // the re-issued tail loads land before the ring is refilled or released
+
+        // ---- part of a tile (stream-K).  Its workgroups, in range order, are lf .. lf + nc - 1, and
+        // its sum is fixed as ((p_{nc-1} + p_{nc-2}) + ...) + p_0 over their partial tiles, so the
+        // result does not depend on which workgroup finishes last.  Each but the last to finish
+        // writes its fp32 partial and then counts itself in cnt[tile]; the one that finds
+        // the other nc - 1 counted adds the tile up and runs the epilogue: into its own registers
+        // when it holds the end of the tile (p_{nc-1}, the usual case: ranges run their segments
+        // from the last), else from memory, its own partial included.
+        if (SKM && (kb != 0 || nk != nk_all)) {
+            const int64_t tb = (int64_t)tile * nk_all;
+            const int lf = sk_owner(tb, U, SK), nc = sk_owner(tb + nk_all - 1, U, SK) - lf + 1, myc = lw - lf;
+            uint32_t *flag = (uint32_t *)(smem + lds_bytes<WK, BM>());
+            // A partial tile is kept in the lanes' own order: register group (i, j, g) of wave w at
+            // 16 (64 (4 (TN (TM w + i) + j) + g) + lane) bytes, so that each store and load moves 1 KB
+            // in whole lines, and the adding workgroup reads exactly what the same lane wrote.  Stores
+            // and loads carry sc1 (agent coherence: through, not into, the XCDs' own L2s), so the
+            // partials need no L2 write-back or invalidation, only the wait for the stores before the
+            // count.
+            const uint32_t lofs = (uint32_t)(wave * (TM * TN * 4 * 1024) + lane * 16);
+            constexpr int SC1 = 16;    // cache-policy bit sc1 of the buffer intrinsics
+            auto slot_rsrc = [&](int l) {
+                const int sl = __builtin_amdgcn_readfirstlane(sk_slot(l, tile, U, SK, nk_all));
+                return raw_rsrc(wa.part + (int64_t)sl * (BM * BN));
+            };
+            // every other workgroup finished: no count to take
+            if (tid == 0) *flag = __hip_atomic_load(wa.cnt + tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            // (through readfirstlane: a value the compiler knows is uniform, so that what depends
+            // on it stays in scalar registers)
+            bool last = __builtin_amdgcn_readfirstlane(*flag) == nc - 1;
+            if (!last || myc != nc - 1) {   // the partial, for the others or to be read back below
+                const __amdgpu_buffer_rsrc_t rs = slot_rsrc(lw);
                 static_for<TM>([&](auto ic) {
-                    constexpr int i = decltype(ic)::value;
-                    static_for<4>([&](auto cc) {
-                        constexpr int c = decltype(cc)::value;
-                        const float v = value(i, j, 4 * g + c, cs[c], bs[c]);
-                        if (live[i] && c < n_left0 - nc) store_elem(rowp[i], nc + c, wa.y_dtype, v);
+                    static_for<TN>([&](auto jc) {
+                        static_for<4>([&](auto gc) {
+                            constexpr int i = decltype(ic)::value, j = decltype(jc)::value, g = decltype(gc)::value;
+                            const v4i v{agpr_read_for_store(acc[i][j][4 * g]), agpr_read_for_store(acc[i][j][4 * g + 1]),
+                                        agpr_read_for_store(acc[i][j][4 * g + 2]), agpr_read_for_store(acc[i][j][4 * g + 3])};
+                            __builtin_amdgcn_raw_buffer_store_b128(v, rs, lofs + ((i * TN + j) * 4 + g) * 1024, 0, SC1);
+                        });
                     });
                 });
-                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (!last) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial is written before the count
+                __syncthreads();
+                if (tid == 0) *flag = atomicAdd(wa.cnt + tile, 1u);
+                __syncthreads();
+                if (__builtin_amdgcn_readfirstlane(*flag) != nc - 1) continue;
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");       // (its own partial, when it wrote one)
+            // add p_c into the registers (or, first, load it), 16 words a lane in flight
+            auto add = [&](int c, bool first) {
+                const __amdgpu_buffer_rsrc_t rs = slot_rsrc(lf + c);
+                constexpr int CH = TM < 4 ? TM : 4;   // row tiles per chunk
+                static_for<TM / CH>([&](auto chc) {
+                    constexpr int ch = decltype(chc)::value;
+                    v4i v[CH][TN][4];
+                    static_for<CH>([&](auto ic) {
+                        static_for<TN>([&](auto jc) {
+                            static_for<4>([&](auto gc) {
+                                constexpr int i = decltype(ic)::value, j = decltype(jc)::value, g = decltype(gc)::value;
+                                v[i][j][g] = __builtin_amdgcn_raw_buffer_load_b128(
+                                    rs, lofs + (((CH * ch + i) * TN + j) * 4 + g) * 1024, 0, SC1);
+                            });
+                        });
+                    });
+                    static_for<CH>([&](auto ic) {
+                        static_for<TN>([&](auto jc) {
+                            static_for<16>([&](auto rc) {
+                                constexpr int i = decltype(ic)::value, j = decltype(jc)::value, r = decltype(rc)::value;
+                                constexpr int ia = CH * ch + i;
+                                const float pv = __int_as_float(v[i][j][r >> 2][r & 3]);
+                                acc[ia][j][r] = first ? pv : __int_as_float(agpr_read(acc[ia][j][r])) + pv;
+                            });
+                        });
+                    });
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            };
+            if (myc != nc - 1) add(nc - 1, true);
+#pragma clang loop unroll(disable)
+            for (int c = nc - 2; c >= 0; c--) add(c, false);
+        }
+
+        // ---- epilogue: acc[i][j] is the transposed 32 x 32 tile, lane (l & 31) holds output row
+        // m = m0 + 32 i + (l & 31), register 4g + c column n = n0 + WCOLS wave + 32 j + 8 g + 4 h + c.
+        //   y = round_out(fmaf(acc, s[n], bias[n]))   (s = 1 for uint4)
+        const int nl0 = WCOLS * wave + 4 * h;                    // the lane's first column in the tile
+        const int esz = wa.y_dtype == PSQ_F32 ? 4 : 2;
+        uint8_t *rowp[TM];
+        bool live[TM];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int m = m0 + 32 * i + frow;
+            live[i] = m < M;
+            rowp[i] = (uint8_t *)wa.y + ((int64_t)min(m, M - 1) * wa.ldy + n0 + nl0) * esz;
+        }
+        // operands of the lane's 4 columns n0 + nl0 + nc .. + 3: the row scale (int8) and the bias
+        auto operands = [&](int nc, float (&cs)[4], float (&bs)[4]) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int n = min(n0 + nl0 + nc + c, N - 1);
+                cs[c] = (WK == W_INT8) ? wa.scale32[n] : 1.0f;
+                bs[c] = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
+            }
+        };
+        auto value = [&](int i, int j, int r, float c, float b) {
+            return __builtin_fmaf(__int_as_float(agpr_read(acc[i][j][r])), c, b);
+        };
+        const bool fast = wa.y_dtype != PSQ_F32 && n0 + BN <= N && ((uintptr_t)wa.y & 15) == 0 && (wa.ldy * 2) % 16 == 0;
+        if (fast) {
+            // lanes l and l + 32 hold the same row: one v_permlane32_swap per word gives lane l columns
+            // 16 pr + 0..7 and lane l + 32 columns 16 pr + 8..15 of the column pair pr, one 16-byte store
+            const bool bf = wa.y_dtype == PSQ_BF16;
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int pr = 0; pr < 2; pr++) {
+                    const int nc = 32 * j + 16 * pr;
+                    float cs[2][4], bs[2][4];
+                    operands(nc, cs[0], bs[0]);
+                    operands(nc + 8, cs[1], bs[1]);
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        uint32_t x0[2], x1[2];
+#pragma unroll
+                        for (int hh = 0; hh < 2; hh++) {
+                            uint32_t *o = hh == 0 ? x0 : x1;
+                            const int r = 8 * pr + 4 * hh;
+                            const float v0 = value(i, j, r, cs[hh][0], bs[hh][0]), v1 = value(i, j, r + 1, cs[hh][1], bs[hh][1]);
+                            const float v2 = value(i, j, r + 2, cs[hh][2], bs[hh][2]), v3 = value(i, j, r + 3, cs[hh][3], bs[hh][3]);
+                            o[0] = bf ? pack_half2<PSQ_BF16>(v0, v1) : pack_half2<PSQ_F16>(v0, v1);
+                            o[1] = bf ? pack_half2<PSQ_BF16>(v2, v3) : pack_half2<PSQ_F16>(v2, v3);
+                        }
+                        uint32_t lo[2], hi[2];
+#pragma unroll
+                        for (int d = 0; d < 2; d++) {
+                            const auto sw = __builtin_amdgcn_permlane32_swap(x0[d], x1[d], false, false);
+                            lo[d] = sw[0];
+                            hi[d] = sw[1];
+                        }
+                        uint8_t *p = rowp[i] + (nc + 4 * h) * 2;
+                        if (live[i]) *(v4i *)p = v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        } else {
+            const int n_left0 = N - (n0 + nl0);
+            static_for<TN>([&](auto jc) {
+                static_for<4>([&](auto gc) {
+                    constexpr int j = decltype(jc)::value, g = decltype(gc)::value, nc = 32 * j + 8 * g;
+                    float cs[4], bs[4];
+                    operands(nc, cs, bs);
+                    static_for<TM>([&](auto ic) {
+                        constexpr int i = decltype(ic)::value;
+                        static_for<4>([&](auto cc) {
+                            constexpr int c = decltype(cc)::value;
+                            const float v = value(i, j, 4 * g + c, cs[c], bs[c]);
+                            if (live[i] && c < n_left0 - nc) store_elem(rowp[i], nc + c, wa.y_dtype, v);
+                        });
+                    });
+                    __builtin_amdgcn_sched_barrier(0);
+                });
             });
-        });
+        }
     }
 }
 
@@ -1045,73 +1147,21 @@ void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t
 
 constexpr int64_t SKINNY_MAX_M = 64;   // largest M of the streaming and skinny kernels
 
-// Split-K reduction: y = round_out(fmaf(((p_0 + p_1) + ...) + p_{S-1}, cs[n], bias[n])) over the
-// partial tiles of the tiled kernel (cs = the int8 row scale, 1 for uint4), the tiled kernel's
-// epilogue on the sum taken in split order.  One thread per 4 consecutive columns of a row; when
-// the row and the bias are aligned for it, the 4 outputs go out as one 8-byte (16-bit outputs) or
-// 16-byte (fp32) store and the bias comes in as one word (per-element 2-byte stores and loads made
-// the reduction of M=128 x N=25600, 33 MB of partials and outputs, take 9.4 us).
-template <int BM>
-__global__ void __launch_bounds__(256)
-wonly_splitk_reduce(const float *__restrict__ part, int S, int M, int N, WArgs wa, int vec)
+// Zeroes the stream-K arrival counters of a launch: a kernel rather than hipMemsetAsync, so that
+// a launch recorded into a HIP graph replays correctly.
+__global__ void __launch_bounds__(256) sk_clear(uint32_t *__restrict__ cnt, int n)
 {
-    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int nq = (N + 3) / 4;
-    if (id >= (int64_t)M * nq) return;
-    const int m = (int)(id / nq), n = (int)(id % nq) * 4;
-    const int nbn = (N + wt::BN - 1) / wt::BN;
-    const int pm = m / BM, pn = n / wt::BN;
-    const float *p = part + ((int64_t)pm * nbn + pn) * S * (BM * wt::BN) + (m - pm * BM) * wt::BN + (n - pn * wt::BN);
-    v4f t = *(const v4f *)p;
-    for (int sp = 1; sp < S; sp++) {
-        const v4f u = *(const v4f *)(p + (int64_t)sp * (BM * wt::BN));
-        t = v4f{t[0] + u[0], t[1] + u[1], t[2] + u[2], t[3] + u[3]};
-    }
-    const int64_t ysz = wa.y_dtype == PSQ_F32 ? 4 : 2;
-    uint8_t *row = (uint8_t *)wa.y + (int64_t)m * wa.ldy * ysz;
-    if (vec && n + 3 < N) {
-        float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (wa.bias) {
-            if (wa.bias_dtype == PSQ_F32) {
-                const v4f bv = *(const v4f *)((const float *)wa.bias + n);
-                b[0] = bv[0]; b[1] = bv[1]; b[2] = bv[2]; b[3] = bv[3];
-            } else {
-                const v2i bv = *(const v2i *)((const uint16_t *)wa.bias + n);
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const uint32_t w = (uint32_t)bv[c >> 1], h16 = (c & 1) ? w >> 16 : w & 0xffffu;
-                    b[c] = wa.bias_dtype == PSQ_BF16 ? bf16_to_f32(h16) : f16_to_f32(h16);
-                }
-            }
-        }
-        float o[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) o[c] = __builtin_fmaf(t[c], wa.scale32 ? wa.scale32[n + c] : 1.0f, b[c]);
-        if (wa.y_dtype == PSQ_F32) {
-            *(v4f *)(row + (int64_t)n * 4) = v4f{o[0], o[1], o[2], o[3]};
-        } else {
-            uint32_t h[4];     // the rounding of store_elem
-#pragma unroll
-            for (int c = 0; c < 4; c++) h[c] = wa.y_dtype == PSQ_BF16 ? f32_to_bf16(o[c]) : f32_to_f16(o[c]);
-            *(v2i *)(row + (int64_t)n * 2) = v2i{(int)(h[0] | (h[1] << 16)), (int)(h[2] | (h[3] << 16))};
-        }
-        return;
-    }
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        if (n + c >= N) break;
-        const float cs = wa.scale32 ? wa.scale32[n + c] : 1.0f;
-        const float b = wa.bias ? load_elem(wa.bias, n + c, wa.bias_dtype) : 0.0f;
-        store_elem(row, n + c, wa.y_dtype, __builtin_fmaf(t[c], cs, b));
-    }
+    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (i < n) cnt[i] = 0u;
 }
 
-template <int XDT, int WK, int BM>
+template <int XDT, int WK, int BM, bool SKM>
 int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
                     const char *name)
 {
-    auto kern = gemm_wonly_tiled<XDT, WK, BM>;
-    constexpr int lds = wt::lds_bytes<WK, BM>();
+    auto kern = gemm_wonly_tiled<XDT, WK, BM, SKM>;
+    constexpr int lds = wt::lds_bytes<WK, BM>() + (SKM ? 16 : 0);   // + the word that broadcasts a stream-K count
+    static_assert(lds <= 163840, "LDS of the tiled kernel");
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
     static bool attr_set[64] = {};   // per device; the attribute is idempotent
@@ -1121,62 +1171,80 @@ int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_
         attr_set[dev] = true;
     }
     const int64_t tiles = ((M + BM - 1) / BM) * ((N + wt::BN - 1) / wt::BN);
-    kern<<<dim3((unsigned)(tiles * wa.ksplit)), dim3(wt::THREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
-    if (wa.ksplit > 1) {
+    if (SKM) {
+        sk_clear<<<dim3((unsigned)((tiles + 255) / 256)), dim3(256), 0, st>>>(wa.cnt, (int)tiles);
         if (int e = check_launch(name)) return e;
-        // whole-quad stores and bias words: 8-byte aligned rows (16-byte for fp32) and bias
-        const int64_t ysz = wa.y_dtype == PSQ_F32 ? 4 : 2, bsz = wa.bias_dtype == PSQ_F32 ? 4 : 2;
-        const int vec = ((uintptr_t)wa.y % (4 * ysz) == 0 && (wa.ldy * ysz) % (4 * ysz) == 0 &&
-                         (!wa.bias || (uintptr_t)wa.bias % (4 * bsz) == 0)) ? 1 : 0;
-        const int64_t quads = M * ((N + 3) / 4);
-        wonly_splitk_reduce<BM><<<dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st>>>(wa.part, wa.ksplit, (int)M,
-                                                                                           (int)N, wa, vec);
     }
+    kern<<<dim3((unsigned)(SKM ? wa.sk : tiles)), dim3(wt::THREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
     return check_launch(name);
 }
 
-#ifndef PSQ_WT_FILL
-#define PSQ_WT_FILL 1
-#endif
-// Split-K cost model: a split of s runs 1/s of a tile's K per workgroup, and each extra split adds
-// its ring prologue and its partial tile's round trip through memory.  Splits stay within one round
-// of workgroups (tiles s <= CUs): at M=1024, N=K=5120 (160 tiles) three splits in two rounds measured slower than
-// none (99 against 89 us), while two splits of M = 128 x N = 25600 (100 tiles) took 89 to 65 us.
-#ifndef PSQ_WT_SPLIT_COST
-#define PSQ_WT_SPLIT_COST 0.05
-#endif
-constexpr int kMaxSplit = 8;
-constexpr int64_t kMaxPartBytes = 64LL << 20;                   // partial tiles of one launch
+// Launch plan of the tiled kernel, in units of one 128-row tile's K stage on a lightly loaded GPU.
+//  * Data-parallel (one tile per workgroup): ceil(tiles / CUs) rounds of nk stages; a 256-row
+//    tile's stage costs about kBm256Cost of a 128-row one (the dequantization serves twice the
+//    rows: at N=25600 x K=5120, 126 us for a 256-row tile against 78 for a 128-row one).
+//  * Stream-K, 128-row tiles only (the 256-row kernel has no registers to spare for it), over G
+//    workgroups: ceil(tiles nk / G) stages each.  With G a multiple s of the tiles, each workgroup
+//    takes one K range of one tile (one partial, written or added up); otherwise up to two
+//    segments (a second ring prologue, two partials).  Each partial costs about kSkPartCost.
+//  * The kernel is power-limited: with more than about 78% of the CUs busy the clock drops, a
+//    stage taking about 1 + 0.6 (busy fraction - 0.78) times as long (M=128 x N=25600: 1.13 us a
+//    stage on 200 CUs, 1.2-1.37 on 256).
+// Stream-K is taken when it beats data-parallel by more than kSkMargin, and needs a workspace:
+// the tiles' arrival counters (kSkCntBytes, room for kSkMaxTiles) and two fp32 partial tiles per
+// workgroup.  Without stream-K, 128-row tiles while they fit one round of workgroups.
+constexpr int kSkMinUnits = 8;                              // K stages per workgroup at least
+constexpr double kSkPartCost = 3.0, kSkRestartCost = 2.0, kSkMargin = 0.9;
+constexpr double kBm256Cost = 1.4;
+constexpr int64_t kSkMaxTiles = 16384;
+constexpr int64_t kSkCntBytes = kSkMaxTiles * 4;
+constexpr int64_t kSkSlotBytes = 128LL * wt::BN * 4;        // one 128-row fp32 partial tile
+constexpr int kSkMaxGroups = 256;
+constexpr int64_t kMaxWsBytes = kSkCntBytes + 2 * kSkMaxGroups * kSkSlotBytes;   // 64 MB + 64 KB
 
-// The tiled kernel's launch: 128-row tiles when they still fit one wave of workgroups on the GPU
-// (twice the tiles of the 256-row ones, each with half the MFMA work and the same
-// dequantization), else 256-row tiles; and, when the tiles leave CUs idle, the K split with the
-// fewest rounds per unit of work.  Workspace: the partial tiles.
+inline double clock_factor(int64_t busy, int cus)
+{
+    const double f = (double)busy / cus - 0.78;
+    return f > 0 ? 1.0 + 0.6 * f : 1.0;
+}
+
 struct TiledPlan {
     int bm = 128;
     int64_t tiles = 0;
-    int ksplit = 1;
+    int sk = 0;                 // stream-K workgroups (0: data-parallel)
     int64_t ws_bytes = 0;
 };
 
-TiledPlan plan_tiled(int64_t M, int64_t N, int64_t K, int cus)
+TiledPlan plan_tiled(int64_t M, int64_t N, int64_t K, int cus, bool allow_sk)
 {
     TiledPlan p;
-    const int64_t nbn = (N + wt::BN - 1) / wt::BN;
-    p.bm = ((M + 127) / 128) * nbn <= PSQ_WT_FILL * cus ? 128 : 256;
+    const int64_t nbn = (N + wt::BN - 1) / wt::BN, nk = K / wt::BK;
+    p.bm = ((M + 127) / 128) * nbn <= cus ? 128 : 256;
     p.tiles = ((M + p.bm - 1) / p.bm) * nbn;
-    const int64_t nk = K / wt::BK;
-    double best = 1.0;
-    if (p.bm == 128 && p.tiles < cus) {   // the kernel splits 128-row tiles
-        for (int s = 2; s <= kMaxSplit && 4 * s <= nk && p.tiles * s <= cus; s++) {
-            const double t = 1.0 / s + PSQ_WT_SPLIT_COST * (s - 1);
-            if (t < best - 1e-9 && p.tiles * s * p.bm * wt::BN * 4 <= kMaxPartBytes) {
-                best = t;
-                p.ksplit = s;
-            }
+    if (!allow_sk) return p;
+    const double t_dp = (double)((p.tiles + cus - 1) / cus * nk) * (p.bm == 256 ? kBm256Cost : 1.0) *
+                        clock_factor(std::min<int64_t>(p.tiles, cus), cus);
+    const int64_t t128 = ((M + 127) / 128) * nbn, units = t128 * nk;
+    if (t128 > kSkMaxTiles) return p;
+    double best = kSkMargin * t_dp;
+    int64_t best_g = 0;
+    auto consider = [&](int64_t g, bool aligned) {
+        if (g < 1 || g > cus || g > kSkMaxGroups || units / g < kSkMinUnits) return;
+        const double t = (double)((units + g - 1) / g) * clock_factor(g, cus) +
+                         (aligned ? kSkPartCost : 2 * kSkPartCost + kSkRestartCost);
+        if (t < best) {
+            best = t;
+            best_g = g;
         }
+    };
+    for (int64_t sp = 2; t128 * sp <= cus; sp++) consider(t128 * sp, true);   // one K range of one tile each
+    consider(cus, false);
+    if (best_g) {
+        p.bm = 128;
+        p.tiles = t128;
+        p.sk = (int)best_g;
+        p.ws_bytes = kSkCntBytes + 2 * best_g * kSkSlotBytes;
     }
-    p.ws_bytes = p.ksplit > 1 ? p.tiles * p.ksplit * p.bm * wt::BN * 4 : 0;
     return p;
 }
 
@@ -1204,10 +1272,11 @@ int64_t workspace_bytes(int wk, int64_t ldx, int64_t M, int64_t N, int64_t K, in
     if (M <= 0 || N <= 0 || K <= 0 || choose_path(wk, ldx, M, K, gs) != Path::Tiled) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    return plan_tiled(M, N, K, cu_count(dev)).ws_bytes;
+    return plan_tiled(M, N, K, cu_count(dev), true).ws_bytes;
 }
 
-// workspace: NULL = no split; else at least workspace_bytes() (no contents carried between calls).
+// workspace: NULL = data-parallel tiles only; else at least workspace_bytes() (no contents carried
+// between calls: the launch clears the counters it uses and writes every partial it reads).
 template <int WK>
 int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_t K, WArgs wa,
            void *workspace, int64_t ws_bytes, hipStream_t st, const char *name)
@@ -1229,21 +1298,22 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
     if (K > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: K above 2^22", name);       // (of the weights too)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
-    const TiledPlan plan = plan_tiled(M, N, K, cu_count(dev));
-    wa.ksplit = 1;
-    if (workspace && plan.ksplit > 1) {
+    const TiledPlan plan = plan_tiled(M, N, K, cu_count(dev), workspace != nullptr);
+    wa.sk = 0;
+    if (plan.sk) {
         if (ws_bytes < plan.ws_bytes)
             return set_error(PSQ_E_ARG, "%s: workspace of %lld bytes, %lld needed", name, (long long)ws_bytes,
                              (long long)plan.ws_bytes);
         if ((uintptr_t)workspace & 255) return set_error(PSQ_E_ARG, "%s: workspace must be 256-byte aligned", name);
-        wa.ksplit = plan.ksplit;
-        wa.part = (float *)workspace;
+        wa.sk = plan.sk;
+        wa.cnt = (uint32_t *)workspace;
+        wa.part = (float *)((uint8_t *)workspace + kSkCntBytes);
     }
-    const bool bm128 = plan.bm == 128;
     auto go = [&](auto xc) {
         constexpr int XDT = decltype(xc)::value;
-        return bm128 ? launch_tiled_bm<XDT, WK, 128>(xp, ldx, M, N, K, wa, st, name)
-                     : launch_tiled_bm<XDT, WK, 256>(xp, ldx, M, N, K, wa, st, name);
+        if (plan.sk) return launch_tiled_bm<XDT, WK, 128, true>(xp, ldx, M, N, K, wa, st, name);
+        return plan.bm == 128 ? launch_tiled_bm<XDT, WK, 128, false>(xp, ldx, M, N, K, wa, st, name)
+                              : launch_tiled_bm<XDT, WK, 256, false>(xp, ldx, M, N, K, wa, st, name);
     };
     return x_dtype == PSQ_BF16 ? go(std::integral_constant<int, PSQ_BF16>{}) : go(std::integral_constant<int, PSQ_F16>{});
 }
@@ -1293,14 +1363,15 @@ int gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t *wq, const 
 }
 
 // ------------------------------------------------------------------ allocation-free variant
-// psq_gemm_w4a16_noalloc keeps its split-K partial tiles in `scratch`, a file-scope device array of
-// the largest workspace any split plan asks for (kMaxPartBytes = 64 MB), held by every GPU the
-// library runs on until the process ends.  In host code `scratch` names a host-side stand-in, not
-// a device address: its address on a device comes from hipGetSymbolAddress, taken once per device
-// with that device current, and only that address is passed to the kernels.  Nothing in it is
-// carried between calls (a call writes every partial it reads), so nothing needs clearing; calls
-// that overlap on one GPU share it and race.
-static __device__ __align__(256) uint8_t scratch[kMaxPartBytes];
+// psq_gemm_w4a16_noalloc keeps its stream-K counters and partial tiles in `scratch`, a file-scope
+// device array of the largest workspace any plan asks for (kMaxWsBytes = 64 MB + 64 KB), held by
+// every GPU the library runs on until the process ends.  In host code `scratch` names a host-side
+// stand-in, not a device address: its address on a device comes from hipGetSymbolAddress, taken
+// once per device with that device current, and only that address is passed to the kernels.
+// Nothing in it is carried between calls: a launch clears the counters it uses with a kernel of
+// its own (no hipMemsetAsync) and writes every partial it reads.  Calls that overlap on one GPU
+// share it and race.
+static __device__ __align__(256) uint8_t scratch[kMaxWsBytes];
 
 constexpr int kMaxDev = 64;
 std::once_flag g_scratch_once[kMaxDev];
@@ -1369,14 +1440,14 @@ int psq_gemm_w4a16_noalloc(const void *x, int x_dtype, int64_t ldx, const uint8_
     if (M > 0 && N > 0 && K > 0) {
         if (int e = require_device()) return e;
         const int64_t need = workspace_bytes(W_UINT4, ldx, M, N, K, group_size);
-        if (need > kMaxPartBytes)
-            return set_error(PSQ_E_SHAPE, "gemm_w4a16_noalloc: %lld bytes of split-K scratch needed, %lld available",
-                             (long long)need, (long long)kMaxPartBytes);
+        if (need > kMaxWsBytes)
+            return set_error(PSQ_E_SHAPE, "gemm_w4a16_noalloc: %lld bytes of stream-K scratch needed, %lld available",
+                             (long long)need, (long long)kMaxWsBytes);
     }
     void *ptr = nullptr;
     if (int e = scratch_on_device(&ptr)) return e;
     return gemm_w4a16(x, x_dtype, ldx, wq, w_scale, w_zero, group_size, bias, bias_dtype, y, y_dtype, ldy, M, N, K,
-                      ptr, kMaxPartBytes, stream, "gemm_w4a16_noalloc");
+                      ptr, kMaxWsBytes, stream, "gemm_w4a16_noalloc");
 }
 
 int64_t psq_gemm_wonly_workspace_bytes(int weight_kind, int64_t ldx, int64_t M, int64_t N, int64_t K, int group_size)

@@ -231,6 +231,14 @@ __device__ __forceinline__ float radix4_lanes_rev(float x)
 }
 
 // ------------------------------------------------------------------ XCD-aware tile order
+// Rank of workgroup pid among n when the ranks of each XCD (pid % 8) are consecutive: a bijection
+// of [0, n) for any n.
+__device__ __forceinline__ int xcd_rank(int pid, int n)
+{
+    const int xcd = pid & 7, per = n >> 3, rem = n & 7;
+    return xcd * per + (xcd < rem ? xcd : rem) + (pid >> 3);
+}
+
 // gfx950 dispatches workgroup i to XCD (i % 8).  Re-number so that each XCD receives a
 // contiguous range of logical tiles, then walk tiles in groups of `group_m` tile rows so
 // that concurrently resident tiles of one XCD share A rows and W rows in its L2.
@@ -298,6 +306,17 @@ __device__ __forceinline__ int agpr_read(float a)
 {
     int v;
     asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+// agpr_read for a value that goes straight into a store.  A VMEM store of more than 8 bytes reads
+// its data registers after issue, and a VALU write of those registers must wait one cycle; the
+// compiler does not reliably count an inline-asm move as such a write, and re-used one store's
+// data registers for the next store's moves at once (the store then wrote the next value for the
+// lanes it had not read yet).  The leading s_nop is that wait.
+__device__ __forceinline__ int agpr_read_for_store(float a)
+{
+    int v;
+    asm volatile("s_nop 0\n\tv_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
     return v;
 }
 

@@ -181,17 +181,21 @@ PSQ_API int psq_gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t
                    int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream);
 
 /* Split-K workspace of the weight-only GEMMs.  When M, N and K leave CUs idle under the tiled
- * kernel (M > 64, e.g. M = 128 at N = 25600: 100 output tiles of 128 x 256 for 256 CUs), the *_ws
- * entry points split each tile's K range over up to 8 workgroups, which write fp32 partial tiles
- * to the workspace; a second kernel on the same stream adds them in split order (a fixed order:
- * results do not depend on timing) and applies the epilogue.  Same outputs and bars as
- * psq_gemm_w4a16 / psq_gemm_w8a16 (a different fp32 summation order).  No counterpart in the
- * reference (the caller-allocated workspace follows the ownership rule above); the callers are
- * the int4 and int8 weight-only linears of the text encoder and Int8Linear.
+ * kernel (M > 64; e.g. M = 128 at N = 25600: 100 output tiles of 128 x 256 for 256 CUs, or M = 1024
+ * at N = K = 5120: 160 tiles), the *_ws entry points split K across workgroups (stream-K): each
+ * tile's K range in a few equal parts, or the (tile, K stage) units of all tiles in equal runs
+ * that cross tile boundaries.  A workgroup holding part of a tile writes its fp32 partial tile to
+ * the workspace and counts itself in the tile's counter there; the last one to finish adds the
+ * partials in K order (a fixed order: results do not depend on timing) and applies the epilogue.
+ * Same outputs and bars as psq_gemm_w4a16 / psq_gemm_w8a16 (a different fp32 summation order).
+ * No counterpart in the reference (the caller-allocated workspace follows the ownership rule
+ * above); the callers are the int4 and int8 weight-only linears of the text encoder and
+ * Int8Linear.
  *   workspace        NULL: no split (exactly psq_gemm_w4a16 / psq_gemm_w8a16); else 256-byte
  *                    aligned and at least psq_gemm_wonly_workspace_bytes() bytes.  Nothing in it
- *                    is carried between calls, but calls that share it must not overlap (use
- *                    one workspace per stream). */
+ *                    is carried between calls (a call clears the counters it uses, with a kernel,
+ *                    and writes every partial it reads), but calls that share it must not overlap
+ *                    (use one workspace per stream). */
 enum psq_weight_kind { PSQ_W_UINT4 = 0, PSQ_W_INT8 = 1 };
 
 /* Bytes of workspace a *_ws call of this shape uses on the current device (0: no split). */
@@ -207,14 +211,14 @@ PSQ_API int psq_gemm_w8a16_ws(const void *x, int x_dtype, int64_t ldx, const int
                       int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *workspace,
                       int64_t workspace_bytes, void *stream);
 
-/* psq_gemm_w4a16_ws without the workspace argument: the split-K partial tiles live in a static
- * device array of the library (64 MB on each GPU it runs on, held until the process ends), so the
- * call allocates nothing -- no hipMalloc, no hipFree, no allocating library routine.  No
- * counterpart in the reference; it is for callers that cannot allocate device memory: code under
- * HIP graph capture, tight serving loops, harnesses that forbid allocation.  Same arguments and
- * results as psq_gemm_w4a16_ws with a large enough workspace.  Every call on one GPU shares that
- * GPU's array: calls that overlap on one GPU race.  A shape whose split plan needs more than the
- * array is refused with PSQ_E_SHAPE (no plan asks for more than 64 MB). */
+/* psq_gemm_w4a16_ws without the workspace argument: the split-K counters and partial tiles live in
+ * a static device array of the library (64 MB + 64 KB on each GPU it runs on, held until the
+ * process ends), so the call allocates nothing -- no hipMalloc, no hipFree, no allocating library
+ * routine.  No counterpart in the reference; it is for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid allocation.
+ * Same arguments and results as psq_gemm_w4a16_ws with a large enough workspace.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU race.  A shape whose split plan
+ * needs more than the array is refused with PSQ_E_SHAPE (no plan asks for more). */
 PSQ_API int psq_gemm_w4a16_noalloc(const void *x, int x_dtype, int64_t ldx, const uint8_t *wq,
                            const uint16_t *w_scale, const uint16_t *w_zero, int group_size,
                            const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,

@@ -289,11 +289,14 @@ def _split_plan(M, N, K, gs, kind=0):
 
 
 @pytest.mark.parametrize("M,N,K,xdt", [(128, 25600, 5120, torch.bfloat16), (100, 2048, 2048, torch.bfloat16),
-                                       (77, 1280, 1024, torch.float16), (200, 520, 4096, torch.bfloat16)])
+                                       (77, 1280, 1024, torch.float16), (200, 520, 4096, torch.bfloat16),
+                                       (1024, 5120, 5120, torch.bfloat16)])
 def test_gemm_w4a16_split_k(gpu, M, N, K, xdt):
-    """Shapes whose 128-row tiles leave CUs idle split K over up to 8 workgroups per tile; the last
-    to arrive adds the fp32 partials in split order.  Same bar as the unsplit kernel, and repeated
-    calls are bit-identical (the order does not depend on which workgroup arrives last)."""
+    """Shapes whose tiles leave CUs idle split K across workgroups (stream-K): each tile's K range
+    in a few parts, or, at 1024 x 5120 x 5120, equal runs of (tile, K stage) units that cross tile
+    boundaries; the last workgroup of a tile to finish adds the fp32 partials in K order.  Same bar
+    as the unsplit kernel, and repeated calls are bit-identical (the order does not depend on
+    which workgroup finishes last)."""
     from powershard_amd import ops
     gs = 128
     assert _split_plan(M, N, K, gs) > 0, "shape expected to split"
@@ -362,10 +365,10 @@ def test_w4a16_dequantized_weights_exact(gpu, M, xdt):
 @pytest.mark.parametrize("out_dt,bias_dt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                             (torch.float32, torch.float32)])
 def test_gemm_w4a16_split_k_output_layouts(gpu, out_dt, bias_dt):
-    """The split-K reduction writes a thread's 4 columns with one store and reads their bias as one
-    word when the rows and the bias allow it, element by element otherwise.  Every layout gives the
-    same bits: padded rows (aligned, N not a multiple of 4: a partial last quad), odd row strides,
-    a bias that starts at an odd element."""
+    """The workgroup that adds up a split tile runs the tiled kernel's epilogue: 16-byte row stores
+    when the tile is whole and the rows are aligned, element stores otherwise (the last, partial
+    column tile; odd row strides).  Every layout gives the same bits: padded rows (aligned, N not
+    a multiple of 4), odd row strides, a bias that starts at an odd element."""
     import ctypes
     from powershard_amd import _native
     M, N, K, gs = 128, 2050, 2048, 128
