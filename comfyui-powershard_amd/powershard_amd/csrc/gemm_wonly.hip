@@ -43,7 +43,7 @@ struct WArgs {
     // tile's workgroups to finish adds the partials in K order and applies the epilogue
     int sk = 0;
     float *part = nullptr;      // [2 sk][BM][256] fp32: the first and the last partial of each workgroup
-    uint32_t *cnt = nullptr;    // [tiles] finished workgroups per tile, zero at launch
+    uint32_t *cnt = nullptr;    // [tiles] finished workgroups per tile: zero at launch, left zero
 };
 
 template <int XDT>
@@ -559,7 +559,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         // its sum is fixed as ((p_{nc-1} + p_{nc-2}) + ...) + p_0 over their partial tiles, so the
         // result does not depend on which workgroup finishes last.  Each but the last to finish
         // writes its fp32 partial and then counts itself in cnt[tile]; the one that finds
-        // the other nc - 1 counted adds the tile up and runs the epilogue: into its own registers
+        // the other nc - 1 counted zeroes the count, adds the tile up and runs the epilogue: into its own registers
         // when it holds the end of the tile (p_{nc-1}, the usual case: ranges run their segments
         // from the last), else from memory, its own partial included.
         if (SKM && (kb != 0 || nk != nk_all)) {
@@ -604,6 +604,9 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
                 __syncthreads();
                 if (__builtin_amdgcn_readfirstlane(*flag) != nc - 1) continue;
             }
+            // every other workgroup of the tile has counted itself and touches the counter no more:
+            // zero it again, for the next launch on this workspace
+            if (tid == 0) __hip_atomic_store(wa.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");       // (its own partial, when it wrote one)
             // add p_c into the registers (or, first, load it), 16 words a lane in flight
             auto add = [&](int c, bool first) {
@@ -1147,14 +1150,6 @@ void launch_skinny(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t
 
 constexpr int64_t SKINNY_MAX_M = 64;   // largest M of the streaming and skinny kernels
 
-// Zeroes the stream-K arrival counters of a launch: a kernel rather than hipMemsetAsync, so that
-// a launch recorded into a HIP graph replays correctly.
-__global__ void __launch_bounds__(256) sk_clear(uint32_t *__restrict__ cnt, int n)
-{
-    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
-    if (i < n) cnt[i] = 0u;
-}
-
 template <int XDT, int WK, int BM, bool SKM>
 int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
                     const char *name)
@@ -1171,10 +1166,6 @@ int launch_tiled_bm(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_
         attr_set[dev] = true;
     }
     const int64_t tiles = ((M + BM - 1) / BM) * ((N + wt::BN - 1) / wt::BN);
-    if (SKM) {
-        sk_clear<<<dim3((unsigned)((tiles + 255) / 256)), dim3(256), 0, st>>>(wa.cnt, (int)tiles);
-        if (int e = check_launch(name)) return e;
-    }
     kern<<<dim3((unsigned)(SKM ? wa.sk : tiles)), dim3(wt::THREADS), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
     return check_launch(name);
 }
@@ -1275,8 +1266,9 @@ int64_t workspace_bytes(int wk, int64_t ldx, int64_t M, int64_t N, int64_t K, in
     return plan_tiled(M, N, K, cu_count(dev), true).ws_bytes;
 }
 
-// workspace: NULL = data-parallel tiles only; else at least workspace_bytes() (no contents carried
-// between calls: the launch clears the counters it uses and writes every partial it reads).
+// workspace: NULL = data-parallel tiles only; else at least workspace_bytes(), its counter words
+// (the first kSkCntBytes) zero when first passed: every launch leaves them zero, and writes every
+// partial it reads.
 template <int WK>
 int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_t K, WArgs wa,
            void *workspace, int64_t ws_bytes, hipStream_t st, const char *name)
@@ -1368,9 +1360,9 @@ int gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t *wq, const 
 // every GPU the library runs on until the process ends.  In host code `scratch` names a host-side
 // stand-in, not a device address: its address on a device comes from hipGetSymbolAddress, taken
 // once per device with that device current, and only that address is passed to the kernels.
-// Nothing in it is carried between calls: a launch clears the counters it uses with a kernel of
-// its own (no hipMemsetAsync) and writes every partial it reads.  Calls that overlap on one GPU
-// share it and race.
+// A `static __device__` array starts zeroed, and every launch leaves its counters zero (the last
+// workgroup of a tile resets the tile's) and writes every partial it reads: nothing needs clearing.
+// Calls that overlap on one GPU share it and race.
 static __device__ __align__(256) uint8_t scratch[kMaxWsBytes];
 
 constexpr int kMaxDev = 64;

@@ -241,7 +241,7 @@ def _workspace(device, stream, nbytes):
     key = (device.index, stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)   # counter words zero once; calls leave them so
         _workspaces[key] = ws
     return ws, ws.numel()
 

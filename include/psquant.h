@@ -192,10 +192,12 @@ PSQ_API int psq_gemm_w8a16(const void *x, int x_dtype, int64_t ldx, const int8_t
  * above); the callers are the int4 and int8 weight-only linears of the text encoder and
  * Int8Linear.
  *   workspace        NULL: no split (exactly psq_gemm_w4a16 / psq_gemm_w8a16); else 256-byte
- *                    aligned and at least psq_gemm_wonly_workspace_bytes() bytes.  Nothing in it
- *                    is carried between calls (a call clears the counters it uses, with a kernel,
- *                    and writes every partial it reads), but calls that share it must not overlap
- *                    (use one workspace per stream). */
+ *                    aligned and at least psq_gemm_wonly_workspace_bytes() bytes, all zero when
+ *                    first passed (hipMemset once after allocating it).  Its first 64 KB hold the
+ *                    tiles' arrival counters, which every call leaves zero again (the last
+ *                    workgroup of a tile resets them); the rest holds partials that a call
+ *                    writes before it reads them.  Keep it for this use only, and do not let
+ *                    calls that share it overlap (use one workspace per stream). */
 enum psq_weight_kind { PSQ_W_UINT4 = 0, PSQ_W_INT8 = 1 };
 
 /* Bytes of workspace a *_ws call of this shape uses on the current device (0: no split). */

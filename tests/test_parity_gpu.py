@@ -380,7 +380,7 @@ def test_gemm_w4a16_split_k_output_layouts(gpu, out_dt, bias_dt):
     bias_store = (torch.randn(N + 1, generator=seeded(102)) * 0.01).to(bias_dt).to(gpu)
     lib = _native.lib()
     nb = lib.psq_gemm_wonly_workspace_bytes(_native.W_UINT4, K, M, N, K, gs)
-    ws = torch.empty(nb, dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=gpu)   # the counter words zero at first use
     st = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     code = {torch.bfloat16: _native.BF16, torch.float16: _native.F16, torch.float32: _native.F32}
@@ -399,6 +399,7 @@ def test_gemm_w4a16_split_k_output_layouts(gpu, out_dt, bias_dt):
         assert torch.equal(bits(aligned), bits(run(ldy, bias_store[:N]))), f"ldy={ldy}: outputs differ"
     shifted = bias_store[1:]                       # starts at an odd element: read element by element
     assert torch.equal(bits(run(N + 2, shifted)), bits(run(N + 2, shifted.clone()))), "odd bias offset"
+    assert torch.count_nonzero(ws[:65536]).item() == 0, "a call left a tile's arrival counter nonzero"
     wd = oracle.dequant_uint4(wq.cpu(), s.cpu(), z.cpu(), gs)
     rows = _sample_rows(M, 32, 103)
     ref = _wonly_rows(x.cpu(), wd, bias_store[:N].cpu(), rows).float()

@@ -39,7 +39,7 @@ def test_noalloc_matches_workspace_entry_point(gpu, shapes):
         b = (torch.randn(N, generator=seeded(K)) * 0.01).to(torch.bfloat16).to(gpu)
         y_ws = torch.empty(M, N, dtype=torch.float32, device=gpu)
         y_na = torch.full((M, N), float("nan"), dtype=torch.float32, device=gpu)
-        ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+        ws = torch.zeros(need, dtype=torch.uint8, device=gpu)   # the counter words zero at first use
         _call(lib.psq_gemm_w4a16_ws, (x, wq, s, z, gs, b, y_ws, M, N, K, st), ws)
         _call(lib.psq_gemm_w4a16_noalloc, (x, wq, s, z, gs, b, y_na, M, N, K, st))
         torch.cuda.synchronize()
