@@ -458,8 +458,18 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
                 return dq_pair_u4<XDT>(nib_split((uint32_t)r.w[j][0][t]), e, r.s[j], r.z[j]);
             } else {
                 const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
-                const int sh = 16 * (e & 1);
-                return pack2<XDT>((float)(int8_t)((p >> sh) & 0xffu), (float)(int8_t)((p >> (sh + 8)) & 0xffu));
+                if constexpr (XDT == PSQ_F16) {
+                    // f16 pair without conversions: each byte, biased by 128, under the exponent of
+                    // 1024 (0x64bb = 1024 + bb) is 1152 + q exactly, and one packed f16 subtraction of
+                    // 1152 leaves q (integers below 2048 are exact in f16): a v_perm_b32 and a
+                    // v_pk_add_f16 per pair
+                    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, p ^ 0x80808080u, (e & 1) ? 0x04030402u : 0x04010400u);
+                    const f16x2_t q = __builtin_bit_cast(f16x2_t, h) - f16x2_t{(_Float16)1152.0f, (_Float16)1152.0f};
+                    return __builtin_bit_cast(uint32_t, q);
+                } else {
+                    const int sh = 16 * (e & 1);
+                    return pack2<XDT>((float)(int8_t)((p >> sh) & 0xffu), (float)(int8_t)((p >> (sh + 8)) & 0xffu));
+                }
             }
         };
 

@@ -362,6 +362,27 @@ def test_w4a16_dequantized_weights_exact(gpu, M, xdt):
     assert bad == 0, f"{bad} of {y.numel()} dequantized weights differ"
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(48, 640, 1024), (160, 640, 1024), (1024, 5120, 5120)])   # skinny; tiled, K in
+def test_w8a16_dequantized_weights_exact(gpu, M, N, K, xdt):                                     # parts; stream-K runs
+    """One-hot activation rows make every W8A16 output one weight times its row scale, fmaf(q, s, 0)
+    rounded once in fp32: pins the int8 -> bf16 conversion and the f16 one (a byte under the
+    exponent of 1024, then a packed f16 subtraction of 1152) for every code, -128 included."""
+    from powershard_amd import ops
+    g = seeded(120)
+    q = torch.randint(-128, 128, (N, K), dtype=torch.int16, generator=g).to(torch.int8)
+    q[0, :256] = torch.arange(-128, 128, dtype=torch.int16).to(torch.int8)   # every code in row 0
+    sc = torch.rand(N, generator=g) * 0.01 + 1e-3
+    cols = (torch.arange(M) * 37 + 5) % K
+    cols[:min(M, 256)] = torch.arange(min(M, 256))        # row 0's codes reach the outputs
+    x = torch.zeros(M, K, dtype=xdt)
+    x[torch.arange(M), cols] = 1
+    y = ops.gemm_w8a16(x.to(gpu), q.to(gpu), sc.to(gpu), None, out_dtype=torch.float32).cpu()
+    want = (q[:, cols].float() * sc[:, None]).T           # one fp32 product each
+    bad = (y != want).sum().item()
+    assert bad == 0, f"{bad} of {y.numel()} int8 weights differ"
+
+
 @pytest.mark.parametrize("out_dt,bias_dt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                             (torch.float32, torch.float32)])
 def test_gemm_w4a16_split_k_output_layouts(gpu, out_dt, bias_dt):
