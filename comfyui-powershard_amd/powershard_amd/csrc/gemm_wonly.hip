@@ -111,6 +111,17 @@ __device__ __forceinline__ uint32_t dq_pair_u4(const Nib4 &v, int e, float s24, 
 }
 constexpr float kTwo24 = 16777216.0f;
 
+// Two int8 weights (bytes 2 hi and 2 hi + 1 of p) as an exact f16 pair without conversions: each
+// byte, biased by 128, under the f16 exponent of 1024 (0x64bb = 1024 + bb) is 1152 + q, and one
+// packed f16 subtraction of 1152 leaves q (integers below 2048 are exact in f16).  A v_perm_b32
+// and a v_pk_add_f16 per pair, where the conversion takes two extracts, two conversions and a pack.
+__device__ __forceinline__ uint32_t i8pair_f16(uint32_t p, int hi)
+{
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, p ^ 0x80808080u, hi ? 0x04030402u : 0x04010400u);
+    const f16x2_t q = __builtin_bit_cast(f16x2_t, h) - f16x2_t{(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(uint32_t, q);
+}
+
 template <int XDT, int WK, int MT>
 __global__ void __launch_bounds__(NTHREADS)
 gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
@@ -189,8 +200,13 @@ gemm_wonly_skinny(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
                     const uint32_t p = r.w[2 * t + e];
-                    hw[2 * e] = pack2<XDT>((float)(int8_t)(p & 0xffu), (float)(int8_t)((p >> 8) & 0xffu));
-                    hw[2 * e + 1] = pack2<XDT>((float)(int8_t)((p >> 16) & 0xffu), (float)(int8_t)(p >> 24));
+                    if constexpr (XDT == PSQ_F16) {
+                        hw[2 * e] = i8pair_f16(p, 0);
+                        hw[2 * e + 1] = i8pair_f16(p, 1);
+                    } else {
+                        hw[2 * e] = pack2<XDT>((float)(int8_t)(p & 0xffu), (float)(int8_t)((p >> 8) & 0xffu));
+                        hw[2 * e + 1] = pack2<XDT>((float)(int8_t)((p >> 16) & 0xffu), (float)(int8_t)(p >> 24));
+                    }
                 }
             }
             const XV wf = __builtin_bit_cast(XV, v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]});
@@ -459,13 +475,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             } else {
                 const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
                 if constexpr (XDT == PSQ_F16) {
-                    // f16 pair without conversions: each byte, biased by 128, under the exponent of
-                    // 1024 (0x64bb = 1024 + bb) is 1152 + q exactly, and one packed f16 subtraction of
-                    // 1152 leaves q (integers below 2048 are exact in f16): a v_perm_b32 and a
-                    // v_pk_add_f16 per pair
-                    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, p ^ 0x80808080u, (e & 1) ? 0x04030402u : 0x04010400u);
-                    const f16x2_t q = __builtin_bit_cast(f16x2_t, h) - f16x2_t{(_Float16)1152.0f, (_Float16)1152.0f};
-                    return __builtin_bit_cast(uint32_t, q);
+                    return i8pair_f16(p, e & 1);
                 } else {
                     const int sh = 16 * (e & 1);
                     return pack2<XDT>((float)(int8_t)((p >> sh) & 0xffu), (float)(int8_t)((p >> (sh + 8)) & 0xffu));
