@@ -44,6 +44,7 @@ SIGNATURES = {
     "psq_dequant_i8_rows": (_I, [_P, _P, _I64, _I64, _I, _P, _I, _P]),
     "psq_dequant_fp8": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _P]),
     "psq_dequant_e5m2": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _P]),
+    "psq_flag_nonfinite": (_I, [_P, _I, _I64, _P, ctypes.c_uint64, _P]),
 }
 
 

@@ -59,6 +59,7 @@ class Int8Linear(nn.Module):
         self.convrot, self.group_size, self.rows = quant["convrot"], quant["group_size"], rows
 
     def forward(self, x):
+        from . import ops
         safe = getattr(self, "_ps_safe", False)
         tracker = getattr(self, "_ps_tracker", None)
         x = x.float() if safe else x.half()
@@ -70,7 +71,7 @@ class Int8Linear(nn.Module):
             # activations line up with a row of H; the tile path never forms x H.  A non-finite
             # kernel output is therefore recomputed on the tiles before it is reported or raised.
             if out is not None:
-                finite = bool(torch.isfinite(out).all())
+                finite = not ops.any_nonfinite(out)
                 if not finite:
                     out = None
         if out is None:
@@ -88,7 +89,7 @@ class Int8Linear(nn.Module):
                 del w
         if tracker is not None:
             tracker.observe(self._ps_finite_slot, out)
-        elif not finite and not torch.isfinite(out).all():
+        elif not finite and (ops.any_nonfinite(out) if out.is_cuda else not torch.isfinite(out).all()):
             raise FloatingPointError("NaN/Inf after the INT8 -> FP16 Linear")
         return out
 

@@ -325,6 +325,29 @@ def dequant_fp8(q, w_scale, out_dtype=torch.bfloat16, e5m2=None):
     return out
 
 
+# ------------------------------------------------------------------ checks
+# Non-finite flags, one per (device, stream), with the last ticket handed out: a call raises the
+# flag to its ticket when it finds a NaN or Inf, and the flag is never cleared.
+_nonfinite = {}
+
+
+def any_nonfinite(t):
+    """True when the CUDA tensor t (bf16 / f16 / f32) holds a NaN or an Inf: one pass over t and an
+    8-byte read back (a synchronization, as `not torch.isfinite(t).all()`, which this replaces where
+    it is checked on every call)."""
+    _need_gpu(t)
+    t = t.contiguous()
+    stream = _stream(t)
+    key = (t.device.index, stream.value)
+    entry = _nonfinite.get(key)
+    if entry is None:
+        entry = _nonfinite[key] = [torch.zeros(1, dtype=torch.int64, device=t.device), 0]
+    entry[1] += 1
+    _launch("flag_nonfinite", _native.lib().psq_flag_nonfinite, _p(t), _dt(t, "t"), t.numel(), _p(entry[0]),
+            entry[1], stream)
+    return int(entry[0].item()) >= entry[1]
+
+
 def device_supported(device):
     device = torch.device(device)
     if device.type != "cuda":

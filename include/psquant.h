@@ -251,6 +251,18 @@ PSQ_API int psq_dequant_fp8(const uint8_t *q, const float *w_scale, int w_scale_
 PSQ_API int psq_dequant_e5m2(const uint8_t *q, const float *w_scale, int w_scale_per_row, int64_t N,
                     int64_t K, void *out, int out_dtype, void *stream);
 
+/* ---------------------------------------------------------------- checks */
+
+/* Raises *flag (a device word) to max(*flag, ticket) when any of the n elements of x (bf16 / f16
+ * / f32, element-aligned) is NaN or +-Inf; one pass over x.  The device side of the output check
+ * that closes Int8Linear.forward (powershard/operations.py:130-131: `not torch.isfinite(out).all()`
+ * raises FloatingPointError), in place of torch's two kernels.  The flag is never cleared: keep one
+ * per stream, zero once, and pass increasing tickets (from 1); the call's elements were all finite
+ * exactly when the flag read after it is below its ticket.  No hipMemsetAsync, so a captured
+ * launch replays correctly. */
+PSQ_API int psq_flag_nonfinite(const void *x, int dtype, int64_t n, unsigned long long *flag,
+                               unsigned long long ticket, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

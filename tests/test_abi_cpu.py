@@ -58,6 +58,9 @@ def _fake(addr=0x10000):
     # negative sizes
     (lambda L: L.psq_dequant_uint4(_fake(), _fake(), _fake(), 128, -1, 512, _fake(), 0, None), -1),
     (lambda L: L.psq_dequant_i8_rows(_fake(), _fake(), 4, 512, 8, _fake(), 0, None), -2),
+    # non-finite flag: tickets start at 1; the flag is an aligned 8-byte word
+    (lambda L: L.psq_flag_nonfinite(_fake(), 1, 16, _fake(), 0, None), -1),
+    (lambda L: L.psq_flag_nonfinite(_fake(), 1, 16, _fake(0x10004), 1, None), -1),
 ])
 def test_argument_errors_are_reported_without_a_device(call, code):
     lib = _native.lib()
@@ -77,6 +80,7 @@ def test_empty_problems_are_no_ops():
     assert lib.psq_gemm_w8a16(None, 0, 128, _fake(), _fake(), None, 0, None, 0, 16, 0, 16, 128, None) == 0
     assert lib.psq_quantize_rows_i8(None, 0, 0, 512, 512, 256, None, None, 512, None, None) == 0
     assert lib.psq_rotate_rows(None, 0, 0, 512, 512, 256, None, 0, 512, None) == 0
+    assert lib.psq_flag_nonfinite(None, 1, 0, _fake(), 1, None) == 0
     # a non-empty problem with a null operand is still an error
     assert lib.psq_gemm_i8(None, 128, _fake(), _fake(), 128, _fake(), None, 0, _fake(), 0, 16, 4, 16, 128, None) == -1
 

@@ -91,3 +91,30 @@ def test_prepared_linears_on_the_gpu_tile_path(gpu, safe):
     native = make(512, 256, True, 256, gpu, seed=74)
     with prepared_linears((native,), budget=1 << 30) as info:
         assert info["prepared_weight_bytes"] == 0 and not hasattr(native, "_ps_prepared")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,offset", [(1, 0), (7, 1), (8, 0), (9, 3), (1000, 5), ((1 << 20) + 3, 2)])
+def test_any_nonfinite_matches_torch(gpu, dtype, n, offset):
+    """ops.any_nonfinite (psq_flag_nonfinite: raw-bit test, flag raised to a per-call ticket) against
+    `not torch.isfinite(t).all()`: all-finite tensors with the type's largest finite values and its
+    subnormals, then one NaN, +Inf or -Inf at the first element, the middle one or the last, with a
+    finite call after each (the flag is never cleared; the ticket tells the calls apart), on views
+    that start off a 16-byte boundary."""
+    from powershard_amd import ops
+    g = seeded(n + offset)
+    base = (torch.randn(n + offset, generator=g) * 10).to(dtype).to(gpu)
+    t = base[offset:]
+    fi = torch.finfo(dtype)
+    t[0] = fi.max
+    t[-1] = -fi.max
+    if n > 2:
+        t[n // 2] = fi.tiny / 4 if dtype != torch.float32 else fi.tiny / 8   # subnormal
+    assert not ops.any_nonfinite(t) and bool(torch.isfinite(t).all())
+    for pos in sorted({0, n // 2, n - 1}):
+        for bad in (float("nan"), float("inf"), float("-inf")):
+            keep = t[pos].item()
+            t[pos] = bad
+            assert ops.any_nonfinite(t), (pos, bad)
+            t[pos] = keep
+            assert not ops.any_nonfinite(t), (pos, bad, "after")
