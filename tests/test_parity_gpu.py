@@ -290,13 +290,13 @@ def _split_plan(M, N, K, gs, kind=0):
 
 @pytest.mark.parametrize("M,N,K,xdt", [(128, 25600, 5120, torch.bfloat16), (100, 2048, 2048, torch.bfloat16),
                                        (77, 1280, 1024, torch.float16), (200, 520, 4096, torch.bfloat16),
-                                       (1024, 5120, 5120, torch.bfloat16)])
+                                       (1024, 5120, 5120, torch.bfloat16), (100, 40960, 4096, torch.bfloat16)])
 def test_gemm_w4a16_split_k(gpu, M, N, K, xdt):
     """Shapes whose tiles leave CUs idle split K across workgroups (stream-K): each tile's K range
-    in a few parts, or, at 1024 x 5120 x 5120, equal runs of (tile, K stage) units that cross tile
-    boundaries; the last workgroup of a tile to finish adds the fp32 partials in K order.  Same bar
-    as the unsplit kernel, and repeated calls are bit-identical (the order does not depend on
-    which workgroup finishes last)."""
+    in a few parts, or equal runs of (tile, K stage) units that cross tile boundaries (1024 x 5120
+    x 5120, and 100 x 40960 x 4096 with its one partial row tile); the last workgroup of a tile to
+    finish adds the fp32 partials in K order.  Same bar as the unsplit kernel, and repeated calls
+    are bit-identical (the order does not depend on which workgroup finishes last)."""
     from powershard_amd import ops
     gs = 128
     assert _split_plan(M, N, K, gs) > 0, "shape expected to split"
@@ -315,8 +315,11 @@ def test_gemm_w4a16_split_k(gpu, M, N, K, xdt):
     assert_fp32_path(y32.cpu()[rows], yb.cpu()[rows], _wonly_rows(x, wd, b, rows), f"w4a16 split-K {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 1024, 2048), (1024, 5120, 5120)])
+@pytest.mark.parametrize("M,N,K", [(200, 1024, 2048), (1024, 5120, 5120), (100, 40960, 4096)])
 def test_gemm_w8a16_split_k(gpu, M, N, K):
+    """K split across workgroups for the int8 weights: 128-row tiles in K parts (200 x 1024 x 2048)
+    and runs of (tile, K stage) units that cross tiles (1024 x 5120 x 5120 and 100 x 40960 x 4096:
+    160 tiles each, too many to split in whole parts on 256 CUs)."""
     from powershard_amd import ops
     x = heavy_rows(M, K, seed=94, outlier_frac=0)
     w = torch.randn(N, K, generator=seeded(95)) * 0.02
