@@ -78,13 +78,16 @@ __device__ __forceinline__ void ubytes_to_f32(uint32_t w, float (&f)[4])
 // exactly: s * 2^24 is an exact fp32 scaling of the fp16 scale and the fma's product is exact
 // (tests/test_parity_gpu.py::test_w4a16_dequantized_weights_exact checks every kernel's weights
 // bit for bit against round_16(fmaf(q, s, -z s)), fp16-subnormal scales included).
-// The eight nibbles of a word (nibble i = k offset i) are split into four such pairs with 7 ops,
-// then one fma_mix per weight: 19 VALU ops per 8 weights with the packs, against 23 for
-// v_cvt_f32_ubyte + v_fma_f32.
-struct Nib4 { uint32_t a, b, c, d; };   // halves (lo, hi): a = k (0, 4), b = (1, 5), c = (2, 6), d = (3, 7)
+// The eight nibbles of a word (nibble i = k offset i) are split into four such pairs with 5 ops:
+// nibbles 0, 4 and (after one shift by 8) 2, 6 masked to the bottom of their halves, nibbles 1, 5
+// and 3, 7 masked where they stand, four bits up: 16 q 2^-24, still an fp16 subnormal, taken with
+// s 2^20 instead of s 2^24 (also exact).  With one fma_mix per weight and the packs: 17 VALU ops
+// per 8 weights, against 19 with four shifted masks and 23 for v_cvt_f32_ubyte + v_fma_f32.
+struct Nib4 { uint32_t a, b, c, d; };   // halves (lo, hi): a = k (0, 4), b = 16 (1, 5), c = (2, 6), d = 16 (3, 7)
 __device__ __forceinline__ Nib4 nib_split(uint32_t p)
 {
-    return Nib4{p & 0x000f000fu, (p >> 4) & 0x000f000fu, (p >> 8) & 0x000f000fu, (p >> 12) & 0x000f000fu};
+    const uint32_t t = p >> 8;
+    return Nib4{p & 0x000f000fu, p & 0x00f000f0u, t & 0x000f000fu, t & 0x00f000f0u};
 }
 __device__ __forceinline__ float mix_lo(uint32_t h2, float s24, float c)
 {
@@ -98,18 +101,19 @@ __device__ __forceinline__ float mix_hi(uint32_t h2, float s24, float c)
     asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s24), "v"(c));
     return r;
 }
-// packed weights of k offsets 2e, 2e + 1: round_16(fmaf(q, s, c)) each, s24 = s * 2^24
+// packed weights of k offsets 2e, 2e + 1: round_16(fmaf(q, s, c)) each, s24 = s * 2^24,
+// s20 = s * 2^20
 template <int XDT>
-__device__ __forceinline__ uint32_t dq_pair_u4(const Nib4 &v, int e, float s24, float c)
+__device__ __forceinline__ uint32_t dq_pair_u4(const Nib4 &v, int e, float s24, float s20, float c)
 {
     switch (e) {
-    case 0: return pack_half2<XDT>(mix_lo(v.a, s24, c), mix_lo(v.b, s24, c));
-    case 1: return pack_half2<XDT>(mix_lo(v.c, s24, c), mix_lo(v.d, s24, c));
-    case 2: return pack_half2<XDT>(mix_hi(v.a, s24, c), mix_hi(v.b, s24, c));
-    default: return pack_half2<XDT>(mix_hi(v.c, s24, c), mix_hi(v.d, s24, c));
+    case 0: return pack_half2<XDT>(mix_lo(v.a, s24, c), mix_lo(v.b, s20, c));
+    case 1: return pack_half2<XDT>(mix_lo(v.c, s24, c), mix_lo(v.d, s20, c));
+    case 2: return pack_half2<XDT>(mix_hi(v.a, s24, c), mix_hi(v.b, s20, c));
+    default: return pack_half2<XDT>(mix_hi(v.c, s24, c), mix_hi(v.d, s20, c));
     }
 }
-constexpr float kTwo24 = 16777216.0f;
+constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 
 // Two int8 weights (bytes 2 hi and 2 hi + 1 of p) as an exact f16 pair without conversions: each
 // byte, biased by 128, under the f16 exponent of 1024 (0x64bb = 1024 + bb) is 1152 + q, and one
@@ -439,9 +443,9 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             return __builtin_bit_cast(XV, *(const v4i *)(smem + slot * SLOT + r * XROW + ((c ^ xsw(r)) << 4)));
         };
         // the lane's packed weights of a stage (its 32 k of each of its two columns) and, for uint4,
-        // the columns' group scale s (held as s 2^24) and -z s: a weight is round_16(fmaf(q, s, -z s)),
-        // one fma_mix per weight (dq_pair_u4)
-        struct WRaw { v4i w[TN][RB / 32]; float s[TN], z[TN]; };
+        // the columns' group scale s (held as s 2^24 and s 2^20) and -z s: a weight is
+        // round_16(fmaf(q, s, -z s)), one fma_mix per weight (dq_pair_u4)
+        struct WRaw { v4i w[TN][RB / 32]; float s[TN], s4[TN], z[TN]; };
         auto read_w = [&](int slot, int kt, WRaw &r) {
             const uint8_t *sl = smem + slot * SLOT + XBYTES;
 #pragma unroll
@@ -460,10 +464,11 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
                         sv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + 4 * n));
                         zv = f16_to_f32(*(const uint32_t *)(sl + BN * RB + BN * 4 + 4 * n));
                     }
-                    r.s[j] = sv * kTwo24;     // s 2^24 for the fp16-subnormal nibbles (dq_pair_u4)
+                    r.s[j] = sv * kTwo24;     // s 2^24 and s 2^20 for the fp16-subnormal nibbles (dq_pair_u4)
+                    r.s4[j] = sv * kTwo20;
                     r.z[j] = -(zv * sv);      // -z s
                 } else {
-                    r.s[j] = 1.0f;
+                    r.s[j] = r.s4[j] = 1.0f;
                     r.z[j] = 0.0f;
                 }
             }
@@ -471,7 +476,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
         // pair e (k = 32 h + 8 t + 2e, +1) of column tile j's weights in k-step t, packed
         auto dq_pair = [&](const WRaw &r, int j, int t, int e) -> uint32_t {
             if constexpr (WK == W_UINT4) {
-                return dq_pair_u4<XDT>(nib_split((uint32_t)r.w[j][0][t]), e, r.s[j], r.z[j]);
+                return dq_pair_u4<XDT>(nib_split((uint32_t)r.w[j][0][t]), e, r.s[j], r.s4[j], r.z[j]);
             } else {
                 const uint32_t p = (uint32_t)r.w[j][t >> 1][2 * (t & 1) + (e >> 1)];
                 if constexpr (XDT == PSQ_F16) {
@@ -859,7 +864,7 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
 
     // block b's operands in registers: activation fragments, packed weights, scale and -z s.
     // Lane group h carries k = 32 KH h + 8 s .. + 7 of the block in k-step s (0 .. 4 KH - 1).
-    struct Ops { XV xf[MT][4 * KHV]; v4i wv[KHV]; float sc, zs; };
+    struct Ops { XV xf[MT][4 * KHV]; v4i wv[KHV]; float sc, sc4, zs; };
     auto read = [&](int slot, Ops &o) {
         const uint8_t *const sl = smem + slot * SL;
 #pragma unroll
@@ -879,7 +884,8 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
         const uint32_t *sz = (const uint32_t *)(sl + XS + WS + 256 * wave);
         const float sv = f16_to_f32(sz[si]);
         o.zs = -(f16_to_f32(sz[32 + si]) * sv);
-        o.sc = sv * kTwo24;                 // s 2^24 (dq_pair_u4)
+        o.sc = sv * kTwo24;                 // s 2^24 and s 2^20 (dq_pair_u4)
+        o.sc4 = sv * kTwo20;
     };
     // w = round_16(fmaf(q, s, -z s)), then the block's MFMAs
     v4f acc[MT];
@@ -894,7 +900,7 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
             const Nib4 v = nib_split((uint32_t)o.wv[t >> 2][t & 3]);
             uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.zs);
+            for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.sc4, o.zs);
             wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
         }
 #pragma unroll
@@ -1029,7 +1035,7 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     wait_vmcnt<LOADS * D>();            // this wave's activation loads (issued first) landed
     stage_barrier();                    // ... and every other wave's
 
-    struct Ops { XV xf[8]; v4i wv[2]; float sc, zs; };
+    struct Ops { XV xf[8]; v4i wv[2]; float sc, sc4, zs; };
     const uint8_t *const xrow_p = smem + (int64_t)min(nr, M - 1) * xr;
     auto read = [&](int b, int slot, Ops &o) {
         const uint8_t *const sl = ring + slot * WSLOT;
@@ -1045,7 +1051,8 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
         const uint32_t *sz = (const uint32_t *)(sl + WBYTES);
         const float sv = f16_to_f32(sz[si]);
         o.zs = -(f16_to_f32(sz[32 + si]) * sv);
-        o.sc = sv * kTwo24;                 // s 2^24 (dq_pair_u4)
+        o.sc = sv * kTwo24;                 // s 2^24 and s 2^20 (dq_pair_u4)
+        o.sc4 = sv * kTwo20;
     };
     v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](const Ops &o) {
@@ -1055,7 +1062,7 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
             const Nib4 v = nib_split((uint32_t)o.wv[t >> 2][t & 3]);
             uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.zs);
+            for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.sc4, o.zs);
             wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
         }
 #pragma unroll
