@@ -51,7 +51,15 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+try:   # the current stream's raw handle without building a torch.cuda.Stream (2.4 -> ~0.3 us a call)
+    from torch._C import _cuda_getCurrentRawStream as _raw_stream
+except ImportError:
+    _raw_stream = None
+
+
 def _stream(t):
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(t.device.index))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
