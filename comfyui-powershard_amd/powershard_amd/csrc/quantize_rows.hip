@@ -147,6 +147,10 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
 #pragma unroll
     for (int c = 0; c < P; c++) act[c] = (c * T + t) * kElemsPerThread < K;
 
+    // The activations are read once, non-temporally: streamed through with normal loads they evict
+    // the codes this kernel writes, and the weights, from the 256 MB memory-side cache just before
+    // the GEMM reads them (M=32760 x K=5120: rotate+quantize then the int8 GEMM 1929 -> 1869 us,
+    // the GEMM in that sequence 1836 -> 1775 us, the quantizer alone 92 -> 97 us).
     float v[R][P][16];
 #pragma unroll
     for (int rr = 0; rr < R; rr++) {
@@ -156,8 +160,8 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
         for (int c = 0; c < P; c++) {
             v4i raw[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
             if (act[c]) {
-                raw[0] = *(const v4i *)(src + (int64_t)c * T * kElemsPerThread);
-                raw[1] = *(const v4i *)(src + (int64_t)c * T * kElemsPerThread + 8);
+                raw[0] = __builtin_nontemporal_load((const v4i *)(src + (int64_t)c * T * kElemsPerThread));
+                raw[1] = __builtin_nontemporal_load((const v4i *)(src + (int64_t)c * T * kElemsPerThread + 8));
             }
             to_f32<DT>(raw, v[rr][c]);
         }
