@@ -138,6 +138,28 @@ def test_quantize_rows_strided_input(gpu):
     assert_bitexact(s, rs, "scale")
 
 
+def test_launch_stream_is_current_stream(gpu):
+    """Every launch takes the handle of torch's current stream on the tensor's device (read raw,
+    without a torch.cuda.Stream object): the default stream, then a side stream under
+    torch.cuda.stream, then the default stream again; and a quantization on the side stream is
+    ordered after the side stream's own writes to its input."""
+    from powershard_amd import ops
+    x = heavy_rows(64, 1024, seed=12).to(gpu)
+    assert ops._stream(x).value == (torch.cuda.current_stream(x.device).cuda_stream or None)
+    side = torch.cuda.Stream(device=x.device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert ops._stream(x).value == side.cuda_stream
+        y = x.clone()
+        y.mul_(3.0)                  # on the side stream, just before the launch reads it
+        q, s = ops.quantize_rows(y, rot_group=256)
+    torch.cuda.current_stream().wait_stream(side)
+    assert ops._stream(x).value == (torch.cuda.current_stream(x.device).cuda_stream or None)
+    rq, rs = oracle.quantize_rows_i8((x * 3.0).cpu(), 256)
+    assert_bitexact(q, rq, "codes on a side stream")
+    assert_bitexact(s, rs, "scale on a side stream")
+
+
 # --------------------------------------------------------------------------- int8
 GEMM_CASES = [
     # (M, N, K)
