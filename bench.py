@@ -177,17 +177,20 @@ def headline(args):
         y = layer(x)
     if not layer._ps_native:
         raise RuntimeError("native path fell back to dequantize")
+    # each kernel alone, back to back on the same stream: events around the loop, not per launch.
+    # These run first: the shader clock ramps up over the first ~30 GEMM launches after an idle
+    # spell, and these loops (untimed for the headline) leave it settled, as in a serving loop,
+    # whatever warm-up count the headline is given.
+    qx, sx = ops.quantize_rows(x, rot_group=256)
+    wq, ws = qt._qdata, qt._params.scale
+    gemm_ms = untimed_kernel_ms(lambda: ops.gemm_i8(qx, sx, wq, ws, b), max(args.steps, 20), 10)
+    quant_ms = untimed_kernel_ms(lambda: ops.quantize_rows(x, rot_group=256), max(args.steps, 20), 3)
     log(f"[bench] headline: warmup {args.warmup}, timing {args.steps} steps")
 
     def step():
         with torch.no_grad():
             layer(x)
     ms = untimed_kernel_ms(step, args.steps, args.warmup)
-    # each kernel alone, back to back on the same stream: events around the loop, not per launch
-    qx, sx = ops.quantize_rows(x, rot_group=256)
-    wq, ws = qt._qdata, qt._params.scale
-    gemm_ms = untimed_kernel_ms(lambda: ops.gemm_i8(qx, sx, wq, ws, b), args.steps, 3)
-    quant_ms = untimed_kernel_ms(lambda: ops.quantize_rows(x, rot_group=256), args.steps, 3)
     ops_per_step = 2.0 * M * N * K
     tops = ops_per_step / (ms * 1e-3) / 1e12
     gemm_tops = ops_per_step / (gemm_ms * 1e-3) / 1e12

@@ -32,26 +32,6 @@
 namespace psq {
 namespace {
 
-// Tuning knobs (compile-time): the tile grouping and the positions of the int8 ring loads.
-#ifndef PSQ_Q8_GROUP_M
-#define PSQ_Q8_GROUP_M 8
-#endif
-#ifndef PSQ_Q8_STAGED
-#define PSQ_Q8_STAGED 1
-#endif
-#ifndef PSQ_Q8_NT
-#define PSQ_Q8_NT 1
-#endif
-#ifndef PSQ_Q8_HOIST
-#define PSQ_Q8_HOIST 1
-#endif
-#ifndef PSQ_Q8_DMA_I8
-#define PSQ_Q8_DMA_I8 2
-#endif
-#ifndef PSQ_Q8_DMA_F8
-#define PSQ_Q8_DMA_F8 0
-#endif
-
 constexpr int BM = 256, BN = 256, BK = 128;   // BK in bytes (= elements for int8/fp8)
 constexpr int NSTAGE = 2;                      // LDS ring slots: the stage computed, the stage loading
 constexpr int NTHREADS = 256;                  // 4 waves, one per SIMD
@@ -60,7 +40,7 @@ constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;   // 4 x 4 MFMA tiles of 32 x 
 constexpr int STAGE_BYTES = BM * BK;                 // one operand, one stage (32 KB)
 constexpr int LOADS = (BM * BK / 1024) / (NTHREADS / 64);   // 1 KB wave loads per operand per stage (8)
 constexpr int LPS = 2 * LOADS;                       // ring loads per wave per stage (16)
-constexpr int GROUP_M = PSQ_Q8_GROUP_M;
+constexpr int GROUP_M = 8;                           // tile rows per raster group
 
 enum { OUT_BF16 = PSQ_BF16, OUT_F16 = PSQ_F16, OUT_F32 = PSQ_F32, OUT_I32 = 3 };
 
@@ -171,27 +151,19 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chu
 // behind MFMA p (0-15) of k-step t, or -1.  Loads behind the last k-step (after the barrier) fill
 // the slot just freed with stage kt + 2 and are numbered first; loads behind the earlier k-steps
 // complete stage kt + 1 in the other slot before the barrier.  The fragment reads of the next
-// k-step go behind MFMAs 0-7.  int8 uses schedule 2: 6 loads behind the even MFMAs 2-12 of the
-// last k-step, 5 behind MFMAs 1, 4, 7, 10, 13 of k-steps 0 and 1 (measured 1% ahead of the others).
+// k-step go behind MFMAs 0-7.  int8: 6 loads behind the even MFMAs 2-12 of the last k-step, 5
+// behind MFMAs 1, 4, 7, 10, 13 of k-steps 0 and 1 (measured 1% ahead of spreading them evenly or
+// of bunching them behind one k-step).  fp8 (two k-steps per stage): the whole of stage kt + 2
+// behind k-step 1, one load per MFMA.
 template <bool FP8>
 constexpr int dma_slot(int t, int p)
 {
     if constexpr (!FP8) {
-        switch (PSQ_Q8_DMA_I8) {
-        case 0: return p >= 8 ? (t == 3 ? p - 8 : t == 0 ? p : -1) : -1;
-        case 1: return (p & 1) ? (t == 3 ? p >> 1 : t == 0 ? 8 + (p >> 1) : -1) : -1;
-        case 2:
-            if (t == 3) return (p >= 2 && p <= 12 && !(p & 1)) ? (p - 2) / 2 : -1;
-            if (t < 2) return (p % 3 == 1) ? 6 + 5 * t + p / 3 : -1;
-            return -1;
-        case 3: return (p & 3) == 1 ? 4 * ((t + 1) & 3) + (p >> 2) : -1;
-        default: return t == 3 ? ((p & 1) ? (p >> 1) : 8 + (p >> 1)) : -1;
-        }
+        if (t == 3) return (p >= 2 && p <= 12 && !(p & 1)) ? (p - 2) / 2 : -1;
+        if (t < 2) return (p % 3 == 1) ? 6 + 5 * t + p / 3 : -1;
+        return -1;
     } else {
-        switch (PSQ_Q8_DMA_F8) {
-        case 0: return t == 1 ? p : -1;
-        default: return t == 1 ? ((p & 1) ? p >> 1 : -1) : (p < 8 ? 8 + p : -1);
-        }
+        return t == 1 ? p : -1;
     }
 }
 template <bool FP8>
@@ -481,7 +453,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             const int nb = n0 + wn * WAVE_N;
             if (nb >= N) return;
             const int ob = nb >> 1;
-            if constexpr (PSQ_Q8_STAGED && (OUT == OUT_BF16 || OUT == OUT_F16)) {
+            if constexpr (OUT == OUT_BF16 || OUT == OUT_F16) {
                 if (ep.vec) {
                     // one 32 x 64 block per row block i, staged through LDS as in the ungated
                     // epilogue below: whole-line stores
@@ -580,8 +552,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                             if (mb + row < M) {
                                 const uint32_t loff = (uint32_t)((row * ep.ldy + 8 * (lane & 7)) * 2);
                                 v4i *dst = (v4i *)((uint8_t *)ep.y + ubase + loff);
-                                if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val[q], dst);
-                                else *dst = val[q];
+                                __builtin_nontemporal_store(val[q], dst);
                             }
                         }
                         __builtin_amdgcn_sched_barrier(0);
@@ -612,7 +583,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                 }
             return;
         }
-        if constexpr (PSQ_Q8_STAGED && (OUT == OUT_BF16 || OUT == OUT_F16)) {
+        if constexpr (OUT == OUT_BF16 || OUT == OUT_F16) {
             if (ep.vec && n0 + BN <= N) {
                 // Full-width tile, aligned rows, 16-bit outputs: the wave's 128 x 128 block leaves
                 // in blocks of 32 rows x 64 columns through its private 4 KB LDS buffer (chunk
@@ -623,43 +594,29 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                 // wave execute in order, so the buffer needs no barrier.
                 uint8_t *const eb = smem + kEpiOffset + wave * EPI_WAVE_BYTES;
                 const int h = lane >> 5;
-                // (fp8 too: at M=32760, N=15360, K=5120 it leaves two VGPRs to scratch in the
-                // epilogue, and still runs 4% faster than reading the operands per row block)
-                constexpr bool HOIST = PSQ_Q8_HOIST;
+                // The half's column operands are read once for all four row blocks (fp8 too: at
+                // M=32760, N=15360, K=5120 that leaves two VGPRs to scratch in the epilogue, and
+                // still runs 4% faster than reading the operands per row block).
 #pragma unroll
                 for (int hj = 0; hj < 2; hj++) {
-                    // with HOIST the half's column operands are read once for all four row blocks
-                    float hws[HOIST ? 2 : 1][HOIST ? 2 : 1][2][4], hbs[HOIST ? 2 : 1][HOIST ? 2 : 1][2][4];
-                    if constexpr (HOIST) {
+                    float hws[2][2][2][4], hbs[2][2][2][4];
 #pragma unroll
-                        for (int jj = 0; jj < 2; jj++)
+                    for (int jj = 0; jj < 2; jj++)
 #pragma unroll
-                            for (int pr = 0; pr < 2; pr++) {
-                                const int nc = 32 * (2 * hj + jj) + 16 * pr;
-                                operands(nc, hws[jj][pr][0], hbs[jj][pr][0]);
-                                operands(nc + 8, hws[jj][pr][1], hbs[jj][pr][1]);
-                            }
-                    }
+                        for (int pr = 0; pr < 2; pr++) {
+                            const int nc = 32 * (2 * hj + jj) + 16 * pr;
+                            operands(nc, hws[jj][pr][0], hbs[jj][pr][0]);
+                            operands(nc + 8, hws[jj][pr][1], hbs[jj][pr][1]);
+                        }
 #pragma unroll
                     for (int i = 0; i < TM; i++) {
 #pragma unroll
                         for (int jj = 0; jj < 2; jj++)
 #pragma unroll
                             for (int pr = 0; pr < 2; pr++) {
-                                const int j = 2 * hj + jj, nc = 32 * j + 16 * pr;
-                                float ws[2][4], bs[2][4];
-                                if constexpr (HOIST) {
-#pragma unroll
-                                    for (int u = 0; u < 2; u++)
-#pragma unroll
-                                        for (int c = 0; c < 4; c++) {
-                                            ws[u][c] = hws[jj][pr][u][c];
-                                            bs[u][c] = hbs[jj][pr][u][c];
-                                        }
-                                } else {
-                                    operands(nc, ws[0], bs[0]);
-                                    operands(nc + 8, ws[1], bs[1]);
-                                }
+                                const int j = 2 * hj + jj;
+                                const float (&ws)[2][4] = hws[jj][pr];
+                                const float (&bs)[2][4] = hbs[jj][pr];
                                 uint32_t x[2], y[2];
 #pragma unroll
                                 for (int hh = 0; hh < 2; hh++) {
@@ -696,8 +653,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                             for (int q = 0; q < 4; q++) {
                                 const uint32_t loff = (uint32_t)(((8 * q + (lane >> 3)) * ep.ldy + 8 * (lane & 7)) * 2);
                                 v4i *dst = (v4i *)((uint8_t *)ep.y + ubase + loff);
-                                if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val[q], dst);
-                                else *dst = val[q];
+                                __builtin_nontemporal_store(val[q], dst);
                             }
                         } else {
 #pragma unroll
@@ -706,8 +662,7 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                                 if (mb + row < M) {
                                     const uint32_t loff = (uint32_t)((row * ep.ldy + 8 * (lane & 7)) * 2);
                                     v4i *dst = (v4i *)((uint8_t *)ep.y + ubase + loff);
-                                    if constexpr (PSQ_Q8_NT) __builtin_nontemporal_store(val[q], dst);
-                                    else *dst = val[q];
+                                    __builtin_nontemporal_store(val[q], dst);
                                 }
                             }
                         }

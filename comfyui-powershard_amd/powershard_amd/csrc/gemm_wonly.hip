@@ -17,10 +17,6 @@
 namespace psq {
 namespace {
 
-#ifndef PSQ_W4_STREAM
-#define PSQ_W4_STREAM 1
-#endif
-
 constexpr int NTHREADS = 256;
 constexpr int KSTAGE = 64;                     // K granularity of every path
 
@@ -281,13 +277,11 @@ template <int WK> constexpr int wdma() { return BN * wrow<WK>() / 1024 / NWAVE; 
 template <int WK> constexpr int szdma() { return WK == W_UINT4 ? 1 : 0; }
 template <int WK, int BM> constexpr int lps() { return xdma<BM>() + wdma<WK>() + szdma<WK>(); }   // 6 / 6 (BM 256)
 template <int WK, int BM> constexpr int slot_bytes() { return xbytes<BM>() + BN * wrow<WK>() + (WK == W_UINT4 ? 2 * BN * 4 : 0); }
-#ifndef PSQ_WT_NS128
-#define PSQ_WT_NS128 3
-#endif
-// ring depth: 3 slots of 256-row stages; up to PSQ_WT_NS128 of the half-size 128-row ones
+// ring depth: 3 slots of 256-row stages, and of the half-size 128-row ones too (deeper rings of
+// 128-row stages measured no faster)
 template <int WK, int BM> constexpr int nstage()
 {
-    return BM == 256 ? 3 : (163840 / slot_bytes<WK, BM>() < PSQ_WT_NS128 ? 163840 / slot_bytes<WK, BM>() : PSQ_WT_NS128);
+    return 163840 / slot_bytes<WK, BM>() < 3 ? 163840 / slot_bytes<WK, BM>() : 3;
 }
 // uint4 group scales and zeros in blocks of SZG groups: per block and column 16 bytes of scales and
 // 16 of zeros (one dense 16-byte load per lane), two blocks buffered past the ring
@@ -780,10 +774,7 @@ template <int MT> constexpr int XSLOT() { return MT * 16 * BLK<MT>() * 2; }   //
 template <int MT> constexpr int WSLOT() { return NW * 16 * BLK<MT>() / 2; }   // weights of a block
 constexpr int SZSLOT = NW * 256;                             // scale / zero words of a block
 template <int MT> constexpr int SLOT() { return XSLOT<MT>() + WSLOT<MT>() + SZSLOT; }
-#ifndef PSQ_W4S_DCAP
-#define PSQ_W4S_DCAP 64
-#endif
-template <int MT> constexpr int D() { return 163840 / SLOT<MT>() - 1 < PSQ_W4S_DCAP ? 163840 / SLOT<MT>() - 1 : PSQ_W4S_DCAP; }   // blocks in flight
+template <int MT> constexpr int D() { return 163840 / SLOT<MT>() - 1; }   // blocks in flight: as many as the LDS holds
 template <int MT> constexpr int lds_bytes() { return (D<MT>() + 1) * SLOT<MT>(); }
 }  // namespace ws
 
@@ -802,7 +793,10 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     const int nb = K / B;
     const int G = K / wa.gs;                                 // groups per row
     const int64_t wld = K / 2;
-    const int row0 = blockIdx.x * ROWS + 16 * wave;         // the wave's first weight row
+    const int wg_row0 = blockIdx.x * ROWS;                   // the workgroup's first weight row
+    const int row0 = wg_row0 + 16 * wave;                    // the wave's first weight row
+    // the weights from the workgroup's first row: lane offsets stay below 128 rows (32 bits)
+    const uint8_t *const wq = wa.wq + (int64_t)wg_row0 * wld;
 
     // ---- ring loads of a block (all global->LDS; rows past N clamp to the last row)
     // weights: the wave's 16 rows x 64 KH bytes in KH loads of 1 KB; lane L of load d fills row
@@ -814,7 +808,7 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     for (int d = 0; d < KHV; d++) {
         const int r = (16 / KHV) * d + lane / (4 * KHV), pc = lane % (4 * KHV);
         const int c = pc ^ ((r >> (3 - KHV)) & (4 * KHV - 1));
-        wo[d] = (uint32_t)(min(row0 + r, N - 1) * wld + c * 16);
+        wo[d] = (uint32_t)((min(row0 + r, N - 1) - wg_row0) * wld + c * 16);
     }
     // scales and zeros: lane L fetches, for array L >> 5 (scale, zero), row (L >> (KH - 1)) & 15
     // and 128-k half L & (KH - 1), one 16-bit value into its 32-bit slot.  The group of half j of
@@ -844,7 +838,7 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     auto issue = [&](int b, int slot) {
         const int bc = min(b, nb - 1);
         uint8_t *const sl = smem + slot * SL;
-        const uint8_t *const wb = wa.wq + (int64_t)bc * (B / 2);
+        const uint8_t *const wb = wq + (int64_t)bc * (B / 2);
 #pragma unroll
         for (int d = 0; d < KHV; d++)
             __builtin_amdgcn_global_load_lds((glb_ptr)(wb + wo[d]), (lds_ptr)(sl + XS + (WS / NW) * wave + 1024 * d), 16,
@@ -995,8 +989,10 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     const int nr = lane & 15, h = lane >> 4;
     const int nb = K / B, G = K / wa.gs, hg = wa.gs / 128;
     const int64_t wld = K / 2, xr = xrow(K);
-    const int row0 = blockIdx.x * ROWS + 16 * wave;
+    const int wg_row0 = blockIdx.x * ROWS, row0 = wg_row0 + 16 * wave;
     uint8_t *const ring = smem + (int64_t)M * xr + (int64_t)wave * D * WSLOT;
+    // the weights from the workgroup's first row: lane offsets stay below 128 rows (32 bits)
+    const uint8_t *const wq = wa.wq + (int64_t)wg_row0 * wld;
 
     // the activations: row m at m * xr, 1 KB per wave load (K % 512 == 0: whole loads per row)
     const int per_row = (int)(2 * (int64_t)K / 1024), nx = M * per_row;
@@ -1010,7 +1006,7 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
 #pragma unroll
     for (int d = 0; d < 2; d++) {
         const int r = 8 * d + lane / 8, pc = lane % 8;
-        wo[d] = (uint32_t)(min(row0 + r, N - 1) * wld + (pc ^ ((r >> 1) & 7)) * 16);
+        wo[d] = (uint32_t)((min(row0 + r, N - 1) - wg_row0) * wld + (pc ^ ((r >> 1) & 7)) * 16);
     }
     const bool szhi = (lane & 1) != 0;
     const uint16_t *const szrow = (lane < 32 ? wa.scale16 : wa.zero16) + (int64_t)min(row0 + ((lane >> 1) & 15), N - 1) * G;
@@ -1020,7 +1016,7 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     auto issue = [&](int b, int slot) {
         const int bc = min(b, nb - 1);
         uint8_t *const sl = ring + slot * WSLOT;
-        const uint8_t *const wb = wa.wq + (int64_t)bc * (B / 2);
+        const uint8_t *const wb = wq + (int64_t)bc * (B / 2);
 #pragma unroll
         for (int d = 0; d < 2; d++)
             __builtin_amdgcn_global_load_lds((glb_ptr)(wb + wo[d]), (lds_ptr)(sl + 1024 * d), 16, 0, 0);
@@ -1277,7 +1273,7 @@ Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
     if (wk == W_UINT4 && M <= wd::MAXM && gs % 128 == 0 && K % 512 == 0 && decode_depth(M, K) > 0 &&
         ldx <= (1LL << 22))
         return Path::Decode;
-    if (wk == W_UINT4 && PSQ_W4_STREAM && M <= SKINNY_MAX_M && gs % 128 == 0 &&
+    if (wk == W_UINT4 && M <= SKINNY_MAX_M && gs % 128 == 0 &&
         K % (M <= 16 ? ws::BLK<1>() : ws::BLK<2>()) == 0 && ldx <= (1LL << 22))
         return Path::Stream;
     if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (wk != W_UINT4 || gs % 32 == 0)) return Path::Skinny;

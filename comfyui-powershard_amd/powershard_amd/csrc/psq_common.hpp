@@ -309,14 +309,15 @@ __device__ __forceinline__ int agpr_read(float a)
     return v;
 }
 // agpr_read for a value that goes straight into a store.  A VMEM store of more than 8 bytes reads
-// its data registers after issue, and a VALU write of those registers must wait one cycle; the
-// compiler does not reliably count an inline-asm move as such a write, and re-used one store's
-// data registers for the next store's moves at once (the store then wrote the next value for the
-// lanes it had not read yet).  The leading s_nop is that wait.
+// its data registers after issue, and a VALU write of those registers must wait first: two wait
+// states on the gfx940 family, gfx950 included (one on earlier gfx9).  The compiler does not
+// reliably count an inline-asm move as such a write, and re-used one store's data registers for
+// the next store's moves at once (the store then wrote the next value for the lanes it had not
+// read yet).  The leading `s_nop 1` (two wait states) is that wait, whatever the schedule.
 __device__ __forceinline__ int agpr_read_for_store(float a)
 {
     int v;
-    asm volatile("s_nop 0\n\tv_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    asm volatile("s_nop 1\n\tv_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
     return v;
 }
 

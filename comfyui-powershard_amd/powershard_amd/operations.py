@@ -70,6 +70,10 @@ class Int8Linear(nn.Module):
             # The kernel path rounds x H to fp16, and |x H| reaches sqrt(g) max|x| where coherent
             # activations line up with a row of H; the tile path never forms x H.  A non-finite
             # kernel output is therefore recomputed on the tiles before it is reported or raised.
+            # That decision reads the output's flag back (an 8-byte read, a synchronization) on
+            # every call, also with a finite tracker attached, whose own checks the reference
+            # defers to one read per forward (fp16_safe.py FiniteTracker.finish): the tracker must
+            # not see an overflow the tile path would not have produced.
             if out is not None:
                 finite = not ops.any_nonfinite(out)
                 if not finite:

@@ -239,8 +239,17 @@ def gemm_fp8(a, a_scale, w, w_scale, bias=None, out_dtype=torch.bfloat16, activa
 
 
 # Split-K workspaces of the weight-only GEMMs, one per (device, stream): calls on one stream run in
-# order, so they can share it; replaced by a larger one when a call needs more.
+# order, so they can share it (calls on two streams would race on its counters).  A call that needs
+# more gets a larger one (at least twice the size, so a stream is replaced a few times at most), and
+# the replaced buffer is kept until the process ends: a launch captured into a graph keeps the
+# address it was given, which must not be handed out again.  At most _MAX_WS_STREAMS streams per
+# device get one; calls on further streams run without a workspace (the data-parallel tiles: the
+# same results, the split of K left out).  For capture and for callers that cannot allocate at all,
+# psq_gemm_w4a16_noalloc uses the library's own static scratch instead.
 _workspaces = {}
+_retired_workspaces = []
+_MAX_WS_STREAMS = 16
+_WS_MIN_BYTES = 1 << 20
 
 
 def _workspace(device, stream, nbytes):
@@ -248,8 +257,13 @@ def _workspace(device, stream, nbytes):
         return None, 0
     key = (device.index, stream)
     ws = _workspaces.get(key)
+    if ws is None and sum(1 for d, _ in _workspaces if d == device.index) >= _MAX_WS_STREAMS:
+        return None, 0
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)   # counter words zero once; calls leave them so
+        size = max(nbytes, _WS_MIN_BYTES, 2 * ws.numel() if ws is not None else 0)
+        if ws is not None:
+            _retired_workspaces.append(ws)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)   # counter words zero once; calls leave them so
         _workspaces[key] = ws
     return ws, ws.numel()
 
