@@ -294,6 +294,13 @@ template <int WK, int BM> constexpr int lds_bytes()
 // activation chunk swizzle: bijective on 8 consecutive rows (32 banks) and on each parity class
 // of 16 consecutive rows (64 banks), so a fragment read (32 rows, one logical chunk) is conflict free
 __device__ __forceinline__ int xsw(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
+// weight chunk swizzle: chunk c of weight row r (2 chunks of a 32-byte uint4 row, 4 of a 64-byte
+// int8 row) sits at c ^ wsw(r).  ds_read_b128 on gfx950 serves a wave in four groups of 16 lanes,
+// the group of lane l given by l >> 5 and the parity of its bits 2-4 (fitted to two in-bounds
+// probes of 22 address patterns, every measured time predicted); the 32 lanes of a fragment read
+// (rows 32 w .. + 31, one chunk) then fall on distinct banks, where the unswizzled rows conflicted
+// two ways (uint4) and four ways (int8).
+template <int WK> __device__ __forceinline__ int wsw(int r) { return WK == W_UINT4 ? (r >> 4) & 1 : (r >> 3) & 3; }
 // Stream-K over U units and G workgroup ranges, range l = [floor(l U / G), floor((l + 1) U / G)):
 // the range holding unit u (the largest l with floor(l U / G) <= u; ranges are never empty when
 // U >= G) ...
@@ -376,7 +383,7 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             const int b = j * NWAVE + wave;
             const int per = 1024 / RB;                          // rows per load (32 / 16)
             const int r = per * b + lane / (64 / per);
-            wo[j] = (uint32_t)(min(r, N - 1 - n0) * wld + (lane % (64 / per)) * 16);
+            wo[j] = (uint32_t)(min(r, N - 1 - n0) * wld + (((lane % (64 / per)) ^ wsw<WK>(r)) << 4));
         }
         const int scol = min(n0 + 64 * (wave & 3) + lane, N - 1);   // scale (waves 0-3) / zero (4-7) column of this lane
         const unsigned spg = WK == W_UINT4 ? (unsigned)(wa.gs / BK) : 1u;   // stages per group
@@ -446,7 +453,8 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
             for (int j = 0; j < TN; j++) {
                 const int n = WCOLS * wave + 32 * j + frow;
 #pragma unroll
-                for (int c = 0; c < RB / 32; c++) r.w[j][c] = *(const v4i *)(sl + n * RB + (RB / 2) * h + 16 * c);
+                for (int c = 0; c < RB / 32; c++)
+                    r.w[j][c] = *(const v4i *)(sl + n * RB + ((((RB / 32) * h + c) ^ wsw<WK>(n)) << 4));
                 if constexpr (WK == W_UINT4) {
                     float sv, zv;
                     if (szblk) {
@@ -746,212 +754,334 @@ gemm_wonly_tiled(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int 
 }
 
 // ------------------------------------------------------ uint4 streaming kernel (M <= 64)
-// The HBM-bound decode / prompt shapes of W4A16 with groups of a multiple of 128.  A workgroup
-// owns 64 or 128 weight rows (output columns, 16 per wave) over the whole K, so every weight byte
-// is read once and the activations once per workgroup; K runs in blocks of 128 (within one group).
-//  * Loads: per block, each wave's 16 rows x 64 bytes of nibbles, their group scales and zeros
-//    and a share of the activation block (16 MT rows x 256 bytes) go global->LDS into a
-//    (D + 1)-slot ring, D blocks ahead; one barrier per block.  Nothing is loaded into registers
-//    ahead of time, so the compiler's own load tracking adds no waits across the loop.
-//  * The lane dequantizes its 32 weights per block, w = round_16(fmaf(q, s, -z s)): one fma per
-//    weight where the other paths compute (q - z) * s, so a weight can differ from theirs by one
-//    16-bit ulp (when the two fp32 values straddle a rounding boundary, about 2^-16 of the
-//    weights) -- far inside the fp32-accumulation bar.  The VALU work per weight (7/8 of an op to
-//    split the nibbles, one fma_mix, half a pack: dq_pair_u4) is what bounds this kernel at small M.
-//  * MFMA 16x16x32 with the activations as the A operand: lane (n = l & 15, h = l >> 4) holds
-//    output column n (its weight row) and rows 4 h .. 4 h + 3 of each 16-row tile.  Lane group h
-//    carries k = 32 h + 8 t .. + 7 of the block in k-step t for both operands.
+// The weight-streaming shapes of W4A16 (a few tokens to a short prompt against the whole weight)
+// with groups of a multiple of 128 and K a multiple of 256.  A workgroup of 8 waves owns 128
+// weight rows (output columns) over the whole K, so every weight byte is read once and the
+// activations once per workgroup.
+//  * Waves: column group cg = w & 3 (32 weight rows, two 16-column MFMA tiles) and block parity
+//    p = w >> 2.  K runs in ring steps of 256: 128-k block 2s of each step goes to the parity-0
+//    waves, block 2s + 1 to the parity-1 waves, and the two partial sums are added once at the end
+//    (parity 0 + parity 1, a fixed order).  Each activation fragment read from LDS feeds two MFMAs
+//    (the wave's two column tiles), so the 4 waves of a parity read the activations of their block
+//    once each -- half the LDS reads of 16 columns per wave -- and 256 k of a weight row is one
+//    whole 128-byte line per load.
+//  * Loads: per step the workgroup's 128 rows x 128 bytes of nibbles, the two blocks' group scales
+//    and zeros and the 16 MT rows x 512 bytes of activations go global->LDS into a ring of NSLOT
+//    steps, NSLOT - 1 steps ahead of the one computed; one barrier per step.  Nothing is loaded into
+//    registers ahead of time, so the compiler's own load tracking adds no waits across the loop.
+//  * Swizzles: ds_read_b128 on gfx950 does not serve 16 consecutive lanes per LDS cycle (an
+//    in-bounds probe of twelve address patterns rules that out), so the 16-byte chunks are placed
+//    with bit shuffles of the row that keep every fragment read conflict free under each lane
+//    grouping consistent with the probe: activation chunk c of row r at c ^ xsw(r) (512-byte rows),
+//    weight chunk c of row r at c ^ wsw(r) (128-byte rows).
+//  * The lane dequantizes its 64 weights per step (two rows x 32 k), w = round_16(fmaf(q, s, -z s))
+//    (dq_pair_u4: 17 VALU ops per 8 weights): one fma where the dequantize kernel computes
+//    (q - z) s, so a weight can differ from it by one 16-bit ulp (about 2^-16 of the weights), far
+//    inside the fp32-accumulation bar.
+//  * MFMA 16x16x32 with the activations as the A operand: lane (n = l & 15, h = l >> 4) holds output
+//    column n of each column tile and rows 4 h .. 4 h + 3 of each 16-row tile; lane group h carries
+//    k = 32 h + 8 t .. + 7 of the block in k-step t for both operands.
 namespace ws {
-// Per row-tile count MT: KH 128-k halves per block (BLK = 128 KH k) and 8 waves of 16 rows.  MT = 1
-// uses 256-k blocks: full 128-byte lines of every weight row per load and twice the bytes in flight
-// per ring slot, which the latency-bound decode shapes need; larger MT keep 128-k blocks so the
-// ring stays deep within the LDS.
-template <int MT> constexpr int KH() { return MT == 1 ? 2 : 1; }
-template <int MT> constexpr int BLK() { return 128 * KH<MT>(); }
 constexpr int ROWS = 128;                                   // weight rows per workgroup
-constexpr int NW = ROWS / 16;                               // waves
-template <int MT> constexpr int XSLOT() { return MT * 16 * BLK<MT>() * 2; }   // activations of a block
-template <int MT> constexpr int WSLOT() { return NW * 16 * BLK<MT>() / 2; }   // weights of a block
-constexpr int SZSLOT = NW * 256;                             // scale / zero words of a block
-template <int MT> constexpr int SLOT() { return XSLOT<MT>() + WSLOT<MT>() + SZSLOT; }
-template <int MT> constexpr int D() { return 163840 / SLOT<MT>() - 1; }   // blocks in flight: as many as the LDS holds
-template <int MT> constexpr int lds_bytes() { return (D<MT>() + 1) * SLOT<MT>(); }
+constexpr int NW = 8;                                       // waves: 4 column groups x 2 parities
+constexpr int STEP = 256;                                   // k per ring step (two 128-k blocks)
+template <int MT> constexpr int XSLOT() { return MT * 16 * STEP * 2; }   // activations of a step
+constexpr int WSLOT = ROWS * STEP / 2;                       // nibbles of a step (16 KB)
+constexpr int SZSLOT = 2 * 2 * ROWS * 4;                     // [scale | zero][parity][row], 32-bit slots
+// Scale / zero loads, by mode SZM:
+//  * SZ_TABLE: the workgroup's whole scale and zero tables (ROWS rows x G groups x 2 bytes each,
+//    contiguous in memory) go to LDS once, ahead of the ring, when they fit SZT_MAX bytes (G a
+//    multiple of 8 up to 40, MT <= 3);
+//  * SZ_BLOCK: blocks of 8 groups (one 16-byte load per row and array: 4 loads per block, issued
+//    with the block's first step into one of two 4 KB buffers past the ring), G a multiple of 8;
+//  * SZ_STEP: each step loads its blocks' values (one 2-byte value per row and array and block),
+//    any G.
+// On gfx950 a global->LDS load costs about the cache lines it touches, and the per-step form reads
+// 64 rows of the [N, G] tables per 256 bytes (~64 lines): at G = 40 about 2/3 of the lines of a
+// step; the block form cuts that eightfold and the table form to nothing.
+enum { SZ_STEP = 0, SZ_TABLE = 1, SZ_BLOCK = 2 };
+constexpr int SZT_MAX = 2 * ROWS * 40 * 2;                   // 20 KB: G <= 40 (K = 5120 at g = 128)
+constexpr int SZB_BYTES = 2 * ROWS * 16;                      // one block of 8 groups, both arrays
+template <int SZM> constexpr int sz_extra() { return SZM == SZ_TABLE ? SZT_MAX : SZM == SZ_BLOCK ? 2 * SZB_BYTES : 0; }
+template <int MT, int SZM> constexpr int SLOT() { return XSLOT<MT>() + WSLOT + (SZM == SZ_STEP ? SZSLOT : 0); }
+template <int MT, int SZM> constexpr int NSLOT() { return (163840 - sz_extra<SZM>()) / SLOT<MT, SZM>(); }
+template <int MT, int SZM> constexpr int lds_bytes() { return NSLOT<MT, SZM>() * SLOT<MT, SZM>() + sz_extra<SZM>(); }
+// the table form keeps a ring of at least three steps (MT <= 3)
+template <int MT> constexpr bool szt_fits() { return NSLOT<MT, SZ_TABLE>() >= 3; }
+// chunk swizzles (see above): row bits (0, 3, 1, 2) -> chunk bits (0, 1, 2, 3), and for the 128-byte
+// weight rows row bits (1, 3, 2) -> chunk bits (0, 1, 2)
+__device__ __forceinline__ int xsw(int r) { return (r & 1) | ((r >> 2) & 2) | ((r << 1) & 4) | ((r << 1) & 8); }
+__device__ __forceinline__ int wsw(int r) { return ((r >> 1) & 1) | ((r >> 2) & 2) | (r & 4); }
 }  // namespace ws
 
-template <int XDT, int MT>
+template <int XDT, int MT, int SZM>
 __global__ void __launch_bounds__(ws::NW * 64)
 gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
 {
     using namespace ws;
-    constexpr int KHV = KH<MT>(), B = BLK<MT>(), DD = D<MT>(), NX = DD + 1;
-    constexpr int XS = XSLOT<MT>(), WS = WSLOT<MT>(), SL = SLOT<MT>();
+    constexpr int NX = NSLOT<MT, SZM>(), DD = NX - 1;        // ring slots; steps in flight
+    constexpr int XS = XSLOT<MT>(), SL = SLOT<MT, SZM>();
+    constexpr bool SZT = SZM == SZ_TABLE;
     static_assert(DD >= 2, "ring too shallow");
+    // a block of scales is read last by step 4 hg (b + 1) - 1 and its buffer refilled with step
+    // 4 hg (b + 2): after the barrier of step 4 hg (b + 2) + 1 - NX, safe while NX <= 4 hg + 2
+    static_assert(SZM != SZ_BLOCK || NX <= 6, "scale blocks need a ring of at most 6 steps");
     using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nr = lane & 15, h = lane >> 4;
-    const int nb = K / B;
-    const int G = K / wa.gs;                                 // groups per row
+    const int cg = wave & 3, par = wave >> 2;
+    const int ns = K / STEP;
+    const int G = K / wa.gs, hg = wa.gs / 128;               // groups per row; 128-k blocks per group
     const int64_t wld = K / 2;
-    const int wg_row0 = blockIdx.x * ROWS;                   // the workgroup's first weight row
-    const int row0 = wg_row0 + 16 * wave;                    // the wave's first weight row
+    const int wg_row0 = blockIdx.x * ROWS;
     // the weights from the workgroup's first row: lane offsets stay below 128 rows (32 bits)
     const uint8_t *const wq = wa.wq + (int64_t)wg_row0 * wld;
 
-    // ---- ring loads of a block (all global->LDS; rows past N clamp to the last row)
-    // weights: the wave's 16 rows x 64 KH bytes in KH loads of 1 KB; lane L of load d fills row
-    // (16 / KH) d + L / (4 KH), physical chunk L % (4 KH), holding logical chunk pc ^ f(row),
-    // f(n) = (n >> (3 - KH)) & (4 KH - 1), so the 16 lanes reading one chunk of 16 rows hit 16
-    // distinct bank groups
-    uint32_t wo[KHV];
+    // ---- ring loads of a step (all global->LDS; rows past N clamp to the last row)
+    // weights: 16 loads of 1 KB = 8 rows x 128 bytes; wave w issues loads 2 w and 2 w + 1.  Lane L
+    // of load d fills row 8 d + L / 8, physical chunk L % 8, holding logical chunk pc ^ wsw(row).
+    uint32_t wo[2];
 #pragma unroll
-    for (int d = 0; d < KHV; d++) {
-        const int r = (16 / KHV) * d + lane / (4 * KHV), pc = lane % (4 * KHV);
-        const int c = pc ^ ((r >> (3 - KHV)) & (4 * KHV - 1));
-        wo[d] = (uint32_t)((min(row0 + r, N - 1) - wg_row0) * wld + c * 16);
+    for (int i = 0; i < 2; i++) {
+        const int r = 8 * (2 * wave + i) + (lane >> 3), pc = lane & 7;
+        wo[i] = (uint32_t)((min(wg_row0 + r, N - 1) - wg_row0) * wld + ((pc ^ wsw(r)) << 4));
     }
-    // scales and zeros: lane L fetches, for array L >> 5 (scale, zero), row (L >> (KH - 1)) & 15
-    // and 128-k half L & (KH - 1), one 16-bit value into its 32-bit slot.  The group of half j of
-    // block b is (KH b + j) / hg (hg = gs / 128 halves per group), kept as a running quotient and
-    // remainder of KH b on the scalar unit (no per-lane division).
-    const bool szhi = (lane & (KHV - 1)) != 0;
-    const uint16_t *const szrow = (lane < 32 ? wa.scale16 : wa.zero16) +
-                                  (int64_t)min(row0 + ((lane >> (KHV - 1)) & 15), N - 1) * G;
-    const int hg = wa.gs / 128;
-    int gq = 0, gr = 0;                                      // KH b = gq hg + gr for the next block issued
-    // activations: 1 KB = (4 / KH) rows x 256 KH bytes; lane L fills row (4 / KH) d + L / (16 KH),
-    // physical chunk L % (16 KH), holding logical chunk pc ^ (row & 15).  Only the row groups
-    // holding rows below M are loaded (rows past M feed output rows that are never stored); wave w
-    // loads groups w, w + NW, ..: xd of them, a wave-uniform count that picks its vmcnt waits.
-    constexpr int RPL = 4 / KHV;                             // activation rows per load
-    constexpr int XDMAX = (16 * MT / RPL + NW - 1) / NW;
-    static_assert(XDMAX <= 2, "at most two activation loads per wave and block");
-    const int nxl = (M + RPL - 1) / RPL;
+    // scales and zeros: wave w fetches array w & 1 (scale, zero) of block parity (w >> 1) & 1 for
+    // rows 64 (w >> 2) + L, one 16-bit value per lane into its 32-bit slot.  The group of block
+    // 2 s + bp is kept as a running quotient and remainder by hg on the scalar unit.
+    const int sz_arr = wave & 1, sz_par = (wave >> 1) & 1, sz_row = 64 * (wave >> 2) + lane;
+    const uint16_t *const szrow = (sz_arr ? wa.zero16 : wa.scale16) + (int64_t)min(wg_row0 + sz_row, N - 1) * G;
+    const int sz_dst = ((2 * sz_arr + sz_par) * ROWS + 64 * (wave >> 2)) * 4;
+    int gq = sz_par / hg, gr = sz_par % hg;                 // block sz_par + 2 s of the next step issued
+    // activations: 8 MT loads of 1 KB = 2 rows x 512 bytes; wave w issues loads w, w + 8, .. whose
+    // rows start below M (xd of them, a wave-uniform count that picks its vmcnt waits).  Lane L fills
+    // row 2 j + L / 32, physical chunk L % 32, holding logical chunk pc ^ xsw(row).  Rows past M feed
+    // output rows that are never stored.
+    constexpr int XDMAX = (8 * MT + NW - 1) / NW;            // MT
+    const int nxl = (M + 1) / 2;
     const int xd = wave < nxl ? min(XDMAX, (nxl - wave + NW - 1) / NW) : 0;
     uint32_t xo[XDMAX];
 #pragma unroll
     for (int i = 0; i < XDMAX; i++) {
-        const int row = RPL * (wave + NW * i) + lane / (16 * KHV), pc = lane % (16 * KHV);
-        xo[i] = (uint32_t)(min(row, M - 1) * ldx * 2 + (pc ^ (row & 15)) * 16);
+        const int row = 2 * (wave + NW * i) + (lane >> 5), pc = lane & 31;
+        xo[i] = (uint32_t)(min(row, M - 1) * ldx * 2 + ((pc ^ xsw(row)) << 4));
     }
-    // blocks are issued in order, once each (past the end: the last block again)
-    auto issue = [&](int b, int slot) {
-        const int bc = min(b, nb - 1);
+    // scale blocks (SZ_BLOCK): waves 0-3 load, per block, array w & 1 for rows 64 (w >> 1) + L, the
+    // 16 bytes of groups 8 b .. 8 b + 7 of the row; buffer (b & 1), [array][row][8 groups]
+    uint8_t *const szb = smem + NX * SL;
+    const uint16_t *const szblk_src = (wave & 1 ? wa.zero16 : wa.scale16) +
+                                      (int64_t)min(wg_row0 + 64 * ((wave >> 1) & 1) + lane, N - 1) * G;
+    const int szblk_dst = ((wave & 1) * ROWS + 64 * ((wave >> 1) & 1)) * 16;
+    // whether this wave issues a scale block with step st (the block's first step)
+    auto sz_extra_at = [&](int st) { return SZM == SZ_BLOCK && wave < 4 && st < ns && st % (4 * hg) == 0; };
+    // steps are issued in order, once each (past the end: the last step again, into a slot nobody
+    // reads any more)
+    auto issue = [&](int st, int slot) {
+        const int sc = min(st, ns - 1);
         uint8_t *const sl = smem + slot * SL;
-        const uint8_t *const wb = wq + (int64_t)bc * (B / 2);
+        const uint8_t *const wb = wq + (int64_t)sc * (STEP / 2);
 #pragma unroll
-        for (int d = 0; d < KHV; d++)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(wb + wo[d]), (lds_ptr)(sl + XS + (WS / NW) * wave + 1024 * d), 16,
-                                             0, 0);
-        const int g0 = min(gq, G - 1), g1 = min(gq + (gr + 1 >= hg ? 1 : 0), G - 1);
-        __builtin_amdgcn_global_load_lds((glb_ptr)(szrow + (szhi ? g1 : g0)), (lds_ptr)(sl + XS + WS + 256 * wave), 2,
-                                         0, 0);
-        gr += KHV;
-        if (gr >= hg) { gr -= hg; gq++; }
-        if (gr >= hg) { gr -= hg; gq++; }
+        for (int i = 0; i < 2; i++)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(wb + wo[i]), (lds_ptr)(sl + XS + 1024 * (2 * wave + i)), 16, 0, 0);
+        if constexpr (SZM == SZ_STEP) {
+            __builtin_amdgcn_global_load_lds((glb_ptr)(szrow + min(gq, G - 1)), (lds_ptr)(sl + XS + WSLOT + sz_dst), 2, 0, 0);
+            gr += 2;
+            if (gr >= hg) { gr -= hg; gq++; }
+            if (gr >= hg) { gr -= hg; gq++; }
+        } else if constexpr (SZM == SZ_BLOCK) {
+            if (sz_extra_at(st)) {
+                const int b = st / (4 * hg);
+                __builtin_amdgcn_global_load_lds((glb_ptr)(szblk_src + b * 8),
+                                                 (lds_ptr)(szb + (b & 1) * SZB_BYTES + szblk_dst), 16, 0, 0);
+            }
+        }
+        const uint8_t *const xb = (const uint8_t *)x + (int64_t)sc * STEP * 2;
 #pragma unroll
         for (int i = 0; i < XDMAX; i++)
-            if (i < xd)
-                __builtin_amdgcn_global_load_lds((glb_ptr)((const uint8_t *)x + (int64_t)bc * B * 2 + xo[i]),
-                                                 (lds_ptr)(sl + 1024 * (wave + NW * i)), 16, 0, 0);
+            if (i < xd) __builtin_amdgcn_global_load_lds((glb_ptr)(xb + xo[i]), (lds_ptr)(sl + 1024 * (wave + NW * i)), 16, 0, 0);
     };
 
-    // block b's operands in registers: activation fragments, packed weights, scale and -z s.
-    // Lane group h carries k = 32 KH h + 8 s .. + 7 of the block in k-step s (0 .. 4 KH - 1).
-    struct Ops { XV xf[MT][4 * KHV]; v4i wv[KHV]; float sc, sc4, zs; };
-    auto read = [&](int slot, Ops &o) {
+    // The next step's weights, scales and -z s go into registers ahead (Ops); the activation
+    // fragments are read from the step's own slot inside compute, one k-step ahead of their MFMAs
+    // (only two k-steps of fragments are live, which keeps MT = 4 within the 256 registers of two
+    // waves per SIMD; the slot is refilled only after the barrier of the next step).
+    struct Ops { v4i wv[2]; float sc[2], sc4[2], zs[2]; };
+    auto read_x = [&](int slot, int t, XV (&xf)[MT]) {
         const uint8_t *const sl = smem + slot * SL;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int t = 0; t < 4 * KHV; t++) {
-                const int row = 16 * mt + nr, c = 4 * KHV * h + t;
-                o.xf[mt][t] = __builtin_bit_cast(XV, *(const v4i *)(sl + row * (B * 2) + ((c ^ (row & 15)) << 4)));
-            }
-#pragma unroll
-        for (int i = 0; i < KHV; i++) {
-            const int c = KHV * h + i;
-            o.wv[i] = *(const v4i *)(sl + XS + (WS / NW) * wave + nr * (B / 2) +
-                                     ((c ^ ((nr >> (3 - KHV)) & (4 * KHV - 1))) << 4));
-        }
-        const int si = (nr << (KHV - 1)) | ((KHV * h) >> 2);
-        const uint32_t *sz = (const uint32_t *)(sl + XS + WS + 256 * wave);
-        const float sv = f16_to_f32(sz[si]);
-        o.zs = -(f16_to_f32(sz[32 + si]) * sv);
-        o.sc = sv * kTwo24;                 // s 2^24 and s 2^20 (dq_pair_u4)
-        o.sc4 = sv * kTwo20;
-    };
-    // w = round_16(fmaf(q, s, -z s)), then the block's MFMAs
-    v4f acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    auto compute = [&](const Ops &o) {
-        // all the block's weight fragments first: the MFMAs then read registers no VALU op still
-        // writes (a fragment register rewritten behind its MFMA costs a wait per k-step)
-        XV wfs[4 * KHV];
-#pragma unroll
-        for (int t = 0; t < 4 * KHV; t++) {
-            const Nib4 v = nib_split((uint32_t)o.wv[t >> 2][t & 3]);
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.sc4, o.zs);
-            wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
-        }
-#pragma unroll
-        for (int t = 0; t < 4 * KHV; t++) {
-            const XV &wf = wfs[t];
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                if constexpr (XDT == PSQ_BF16)
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.xf[mt][t], wf, acc[mt], 0, 0, 0);
-                else
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.xf[mt][t], wf, acc[mt], 0, 0, 0);
-            }
+        for (int mt = 0; mt < MT; mt++) {
+            const int row = 16 * mt + nr, c = 16 * par + 4 * h + t;
+            xf[mt] = __builtin_bit_cast(XV, *(const v4i *)(sl + row * (STEP * 2) + ((c ^ xsw(row)) << 4)));
         }
     };
-    // a block landed for every wave (own loads per block: KH + 1 + xd; `younger` blocks after it)
-    auto wait_block = [&](auto youngerc) {
-        constexpr int younger = decltype(youngerc)::value, L = KHV + 1;
-        if (xd == 0) wait_vmcnt<younger * L>();
-        else if (XDMAX == 1 || xd == 1) wait_vmcnt<younger * (L + 1)>();
-        else wait_vmcnt<younger * (L + 2)>();
+    // the group of this wave's block of step s (2 s + par), as a running quotient and remainder by
+    // hg (table form; steps are read in order)
+    int tq = par / hg, tr = par % hg;
+    const uint16_t *const szt = (const uint16_t *)(smem + NX * SL);     // [scale | zero][row][G]
+    auto read_w = [&](int slot, Ops &o) {
+        const uint8_t *const sl = smem + slot * SL;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int row = 32 * cg + 16 * j + nr, c = 4 * par + h;
+            o.wv[j] = *(const v4i *)(sl + XS + row * (STEP / 2) + ((c ^ wsw(row)) << 4));
+            float sv, zv;
+            if constexpr (SZT) {
+                sv = f16_to_f32(szt[row * G + tq]);
+                zv = f16_to_f32(szt[(ROWS + row) * G + tq]);
+            } else if constexpr (SZM == SZ_BLOCK) {
+                const uint16_t *bb = (const uint16_t *)(szb + ((tq >> 3) & 1) * SZB_BYTES) + (tq & 7);
+                sv = f16_to_f32(bb[row * 8]);
+                zv = f16_to_f32(bb[(ROWS + row) * 8]);
+            } else {
+                const uint32_t *sz = (const uint32_t *)(sl + XS + WSLOT);
+                sv = f16_to_f32(sz[par * ROWS + row]);
+                zv = f16_to_f32(sz[(2 + par) * ROWS + row]);
+            }
+            o.zs[j] = -(zv * sv);
+            o.sc[j] = sv * kTwo24;             // s 2^24 and s 2^20 (dq_pair_u4)
+            o.sc4[j] = sv * kTwo20;
+        }
+        if constexpr (SZM != SZ_STEP) {
+            tr += 2;
+            if (tr >= hg) { tr -= hg; tq++; }
+            if (tr >= hg) { tr -= hg; tq++; }
+        }
+    };
+    v4f acc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[mt][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    // Step in `slot` with weights `o`: the first k-step's fragments are issued, then all the
+    // step's weight fragments dequantized (the MFMAs then read registers no VALU op still writes; a
+    // fragment register rewritten behind its MFMA costs a wait per k-step), then per k-step the
+    // next k-step's fragments and this one's MFMAs.
+    auto compute = [&](int slot, const Ops &o) {
+        XV xf[2][MT];
+        read_x(slot, 0, xf[0]);
+        XV wfs[2][4];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const Nib4 v = nib_split((uint32_t)o.wv[j][t]);
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc[j], o.sc4[j], o.zs[j]);
+                wfs[j][t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+            }
+        static_for<4>([&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            if constexpr (t + 1 < 4) read_x(slot, t + 1, xf[(t + 1) & 1]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    if constexpr (XDT == PSQ_BF16)
+                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[t & 1][mt], wfs[j][t], acc[mt][j], 0, 0, 0);
+                    else
+                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[t & 1][mt], wfs[j][t], acc[mt][j], 0, 0, 0);
+                }
+        });
+    };
+    // step s landed for every wave: this wave's loads per step are 2 + xd (+ 1 per step, SZ_STEP; + 1
+    // with the first step of a scale block, waves 0-3, SZ_BLOCK: at most one such step among the
+    // `younger` steps issued after s, which are fewer than 4 hg), then the barrier
+    auto wait_step = [&](auto youngerc, int s) {
+        constexpr int younger = decltype(youngerc)::value, L = SZM == SZ_STEP ? 3 : 2;
+        int extra = 0;
+        if constexpr (SZM == SZ_BLOCK) {
+#pragma unroll
+            for (int q = 1; q <= younger; q++) extra += sz_extra_at(s + q) ? 1 : 0;
+        }
+        const int sel = xd + (extra ? 5 : 0);
+        switch (sel) {
+        case 0: wait_vmcnt<younger * L>(); break;
+        case 1: wait_vmcnt<younger * (L + 1)>(); break;
+        case 2: wait_vmcnt<younger * (L + 2)>(); break;
+        case 3: wait_vmcnt<younger * (L + 3)>(); break;
+        case 4: wait_vmcnt<younger * (L + 4)>(); break;
+        case 5: wait_vmcnt<younger * L + 1>(); break;
+        case 6: wait_vmcnt<younger * (L + 1) + 1>(); break;
+        case 7: wait_vmcnt<younger * (L + 2) + 1>(); break;
+        case 8: wait_vmcnt<younger * (L + 3) + 1>(); break;
+        default: wait_vmcnt<younger * (L + 4) + 1>(); break;
+        }
         stage_barrier();
     };
 
-    // Software pipeline: the LDS reads of block b + 1 are issued before block b's dequantization
-    // and MFMAs, which cover their latency.  Block b's slot is refilled once every wave has passed
-    // the barrier of block b + 1 (it read block b before that).
-#pragma unroll
-    for (int b = 0; b < DD; b++) issue(b, b);
-    Ops oa, ob;
-    wait_block(std::integral_constant<int, DD - 1>{});
-    read(0, oa);
-    int rslot = 1, fslot = DD;                               // slot of block b + 1, slot to refill
-    auto step = [&](int b, const Ops &cur, Ops &nxt) {
-        if (b + 1 < nb) {
-            wait_block(std::integral_constant<int, DD - 2>{});
-            read(rslot, nxt);
-            rslot = rslot == NX - 1 ? 0 : rslot + 1;
+    // Software pipeline: step s + 1 is waited for (and its weights read) before step s computes, so
+    // the LDS reads overlap step s's work.  A step's activation fragments are read while it
+    // computes, so the slot of step s - 1 is refilled (with step s - 1 + NX) only after the barrier
+    // of step s, which every wave reaches after finishing step s - 1; the last step has no barrier
+    // and refills nothing.  Past the end the refills load the last step again (the vmcnt waits count
+    // a constant number of younger steps).
+    if constexpr (SZT) {
+        // the tables: ROWS G halves per array, contiguous from the workgroup's first row, in 1 KB
+        // loads spread over the waves; lanes past the last row read the last 16 bytes instead (their
+        // columns are never stored).  Issued before step 0, so step 0's wait covers them (loads
+        // complete in order).
+        const int tb = ROWS * G * 2, nl = (tb + 1023) / 1024;
+        const int64_t valid = (int64_t)min(ROWS, N - wg_row0) * G * 2;
+        for (int i = wave; i < 2 * nl; i += NW) {
+            const int arr = i >= nl, off = (i - arr * nl) * 1024 + 16 * lane;
+            const uint8_t *src = (const uint8_t *)((arr ? wa.zero16 : wa.scale16) + (int64_t)wg_row0 * G);
+            if (off < tb)
+                __builtin_amdgcn_global_load_lds((glb_ptr)(src + min((int64_t)off, valid - 16)),
+                                                 (lds_ptr)(smem + NX * SL + arr * tb + (i - arr * nl) * 1024), 16, 0, 0);
         }
-        issue(b + DD, fslot);
-        fslot = fslot == NX - 1 ? 0 : fslot + 1;
-        compute(cur);
-    };
-    for (int b = 0; b < nb; b += 2) {
-        step(b, oa, ob);
-        if (b + 1 < nb) step(b + 1, ob, oa);
     }
+#pragma unroll
+    for (int st = 0; st < DD; st++) issue(st, st);
+    Ops oa, ob;
+    wait_step(std::integral_constant<int, DD - 1>{}, 0);
+    read_w(0, oa);
+    int cslot = 0, fslot = DD;                               // slot of step s, slot to refill
+    auto step = [&](int st, const Ops &cur, Ops &nxt) {
+        const int nslot = cslot == NX - 1 ? 0 : cslot + 1;
+        if (st + 1 < ns) {
+            wait_step(std::integral_constant<int, DD - 2>{}, st + 1);
+            read_w(nslot, nxt);
+            issue(st - 1 + NX, fslot);
+            fslot = fslot == NX - 1 ? 0 : fslot + 1;
+        }
+        compute(cslot, cur);
+        cslot = nslot;
+    };
+    for (int st = 0; st < ns; st += 2) {
+        step(st, oa, ob);
+        if (st + 1 < ns) step(st + 1, ob, oa);
+    }
+    // the two parities' partial sums: parity 1 writes, parity 0 adds (fixed order), once every load
+    // has landed and every wave is done with the ring
     wait_vmcnt<0>();
-    // y[m][n] = round_out(acc + bias[n]); lane: n = its row, m = 16 mt + 4 h + v
-    const int n = row0 + nr;
-    if (n < N) {
+    __syncthreads();
+    float *const red = (float *)smem + cg * (MT * 2 * 4 * 64);
+    if (par == 1) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) red[((mt * 2 + j) * 4 + v) * 64 + lane] = acc[mt][j][v];
+    }
+    __syncthreads();
+    if (par == 1) return;
+    // y[m][n] = round_out((acc_0 + acc_1) + bias[n]); lane: n = column tile j's row nr, m = 16 mt + 4 h + v
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int n = wg_row0 + 32 * cg + 16 * j + nr;
+        if (n >= N) continue;
         const float bb = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int m = 16 * mt + 4 * h + v;
-                if (m < M) store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype, acc[mt][v] + bb);
+                if (m < M)
+                    store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype,
+                               (acc[mt][j][v] + red[((mt * 2 + j) * 4 + v) * 64 + lane]) + bb);
             }
     }
 }
@@ -975,6 +1105,11 @@ constexpr int WSLOT = WBYTES + 256;                   // + its scale / zero word
 constexpr int MAXM = 8;
 constexpr int LOADS = 3;                              // ring loads per wave and block
 __host__ __device__ inline int64_t xrow(int64_t K) { return 2 * K + 16; } // padded activation row in LDS (bytes)
+// The wave's 16 weight rows are 128 bytes each, lane (n, h) reading chunks 2 h and 2 h + 1 of row n:
+// chunk c of row r sits at c ^ dsw(r), row bits (3, 1, 2) -> chunk bits (0, 1, 2), a placement free of
+// bank conflicts under every ds_read_b128 lane grouping an in-bounds probe of the LDS allows (the
+// earlier c ^ ((r >> 1) & 7) conflicted two ways).
+__device__ __forceinline__ int dsw(int r) { return ((r >> 3) & 1) | (r & 6); }
 inline int64_t lds_bytes(int64_t M, int64_t K, int D) { return M * xrow(K) + (int64_t)NW * D * WSLOT; }
 }  // namespace wd
 
@@ -1006,7 +1141,7 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
 #pragma unroll
     for (int d = 0; d < 2; d++) {
         const int r = 8 * d + lane / 8, pc = lane % 8;
-        wo[d] = (uint32_t)((min(row0 + r, N - 1) - wg_row0) * wld + (pc ^ ((r >> 1) & 7)) * 16);
+        wo[d] = (uint32_t)((min(row0 + r, N - 1) - wg_row0) * wld + ((pc ^ dsw(r)) << 4));
     }
     const bool szhi = (lane & 1) != 0;
     const uint16_t *const szrow = (lane < 32 ? wa.scale16 : wa.zero16) + (int64_t)min(row0 + ((lane >> 1) & 15), N - 1) * G;
@@ -1041,7 +1176,7 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int c = 2 * h + i;
-            o.wv[i] = *(const v4i *)(sl + nr * (B / 2) + ((c ^ ((nr >> 1) & 7)) << 4));
+            o.wv[i] = *(const v4i *)(sl + nr * (B / 2) + ((c ^ dsw(nr)) << 4));
         }
         const int si = (nr << 1) | (h >> 1);
         const uint32_t *sz = (const uint32_t *)(sl + WBYTES);
@@ -1130,12 +1265,13 @@ int launch_decode(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t 
     return launch_decode_d<XDT, 4>(x, ldx, M, N, K, wa, st, name);
 }
 
-template <int XDT, int MT>
+template <int XDT, int MT, int SZM>
 int launch_stream_mt(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
                      const char *name)
 {
-    auto kern = gemm_w4_stream<XDT, MT>;
-    constexpr int lds = ws::lds_bytes<MT>();
+    auto kern = gemm_w4_stream<XDT, MT, SZM>;
+    constexpr int lds = ws::lds_bytes<MT, SZM>();
+    static_assert(lds <= 163840, "LDS of the streaming kernel");
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
     static bool attr_set[64] = {};
@@ -1149,15 +1285,30 @@ int launch_stream_mt(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64
     return check_launch(name);
 }
 
+// The scale / zero form: the table when the workgroup's tables fit beside a ring of three steps, the
+// 8-group blocks otherwise; both need 16-byte-aligned tables whose rows are whole 16-byte chunks (G a
+// multiple of 8; the clamped loads of the last workgroup then stay aligned and inside its rows).
+template <int XDT, int MT>
+int launch_stream_m(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
+                    const char *name)
+{
+    const int64_t G = K / wa.gs;
+    const bool dense = G % 8 == 0 && ((uintptr_t)wa.scale16 & 15) == 0 && ((uintptr_t)wa.zero16 & 15) == 0;
+    if constexpr (ws::szt_fits<MT>())
+        if (dense && 2 * ws::ROWS * G * 2 <= ws::SZT_MAX) return launch_stream_mt<XDT, MT, ws::SZ_TABLE>(x, ldx, M, N, K, wa, st, name);
+    if (dense) return launch_stream_mt<XDT, MT, ws::SZ_BLOCK>(x, ldx, M, N, K, wa, st, name);
+    return launch_stream_mt<XDT, MT, ws::SZ_STEP>(x, ldx, M, N, K, wa, st, name);
+}
+
 template <int XDT>
 int launch_stream(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
                   const char *name)
 {
     const int mt = (int)((M + 15) / 16);
-    if (mt == 1) return launch_stream_mt<XDT, 1>(x, ldx, M, N, K, wa, st, name);
-    if (mt == 2) return launch_stream_mt<XDT, 2>(x, ldx, M, N, K, wa, st, name);
-    if (mt == 3) return launch_stream_mt<XDT, 3>(x, ldx, M, N, K, wa, st, name);
-    return launch_stream_mt<XDT, 4>(x, ldx, M, N, K, wa, st, name);
+    if (mt == 1) return launch_stream_m<XDT, 1>(x, ldx, M, N, K, wa, st, name);
+    if (mt == 2) return launch_stream_m<XDT, 2>(x, ldx, M, N, K, wa, st, name);
+    if (mt == 3) return launch_stream_m<XDT, 3>(x, ldx, M, N, K, wa, st, name);
+    return launch_stream_m<XDT, 4>(x, ldx, M, N, K, wa, st, name);
 }
 
 template <int XDT, int WK>
@@ -1273,8 +1424,7 @@ Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
     if (wk == W_UINT4 && M <= wd::MAXM && gs % 128 == 0 && K % 512 == 0 && decode_depth(M, K) > 0 &&
         ldx <= (1LL << 22))
         return Path::Decode;
-    if (wk == W_UINT4 && M <= SKINNY_MAX_M && gs % 128 == 0 &&
-        K % (M <= 16 ? ws::BLK<1>() : ws::BLK<2>()) == 0 && ldx <= (1LL << 22))
+    if (wk == W_UINT4 && M <= SKINNY_MAX_M && gs % 128 == 0 && K % ws::STEP == 0 && ldx <= (1LL << 22))
         return Path::Stream;
     if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (wk != W_UINT4 || gs % 32 == 0)) return Path::Skinny;
     return Path::Tiled;

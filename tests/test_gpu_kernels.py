@@ -279,15 +279,19 @@ def test_gemm_fp8(gpu, M, N, K, per_row):
 
 
 # ------------------------------------------------------------------- weight-only
-# M <= 64 runs a weight-streaming kernel (groups of a multiple of 128: the linearity one; else,
-# with K % 128 == 0, the split-K one), the rest the tiled one
+# M <= 64 runs a weight-streaming kernel (groups of a multiple of 128 and K of 256: the streaming
+# one -- its scale / zero tables whole in LDS when K / g is a multiple of 8 up to 40 and M <= 48, in
+# blocks of 8 groups for other multiples of 8, per step otherwise; else, with K % 128 == 0, the
+# split-K one), the rest the tiled one
 @pytest.mark.parametrize("M,N,K,gs", [(512, 384, 1024, 128), (7, 256, 512, 64), (130, 100, 5120, 128),
                                       (64, 1000, 256, 256), (1, 2600, 5120, 128), (16, 513, 1024, 128),
                                       (33, 64, 2048, 64), (65, 300, 1024, 128), (3, 100, 384, 64),
                                       (600, 512, 2048, 256), (300, 768, 320, 64), (1, 256, 192, 64),
                                       (257, 1280, 1024, 512), (2, 300, 1280, 128), (40, 700, 2560, 256),
                                       (64, 129, 640, 128), (17, 1100, 5120, 128), (48, 256, 1536, 384),
-                                      (9, 200, 768, 384), (5, 200, 640, 128), (16, 1024, 5120, 128)])
+                                      (9, 200, 768, 384), (5, 200, 640, 128), (16, 1024, 5120, 128),
+                                      (40, 700, 4096, 128), (24, 1300, 2048, 256), (56, 384, 5120, 128),
+                                      (12, 600, 12288, 128), (50, 256, 8192, 256), (60, 200, 3072, 256)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
     from powershard_amd import ops
