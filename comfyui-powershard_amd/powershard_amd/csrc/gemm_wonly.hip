@@ -1086,48 +1086,80 @@ gemm_w4_stream(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     }
 }
 
-// ------------------------------------------------------ uint4 decode kernel (M <= 4)
-// Decode shapes (a few tokens against the whole weight).  A workgroup of 8 waves owns 128 weight
-// rows, 16 per wave, over the whole K, as in the streaming kernel above, but the waves never
-// meet after the start:
-//  * the activations (M rows, at most a few tens of KB) are loaded into LDS once, behind one
-//    barrier;
-//  * each wave streams its own 16 rows (2 KB of nibbles per 256-k block) and their scales and zeros
-//    through a private LDS ring of D blocks that it alone fills and reads, so a block is ready when
-//    the wave's own load counter says so -- no barrier per block, and no wave waits for another.
+// ------------------------------------------------------ uint4 decode kernel (M <= 8)
+// Decode shapes (a few tokens against the whole weight).  Work items are (16-column unit, 256-k
+// block) pairs, unit after unit.  One workgroup per CU (8 waves) takes a contiguous range of units
+// (U / G of them, G = min(CUs, units)), loads the activations (M rows, at most 80 KB at K = 5120)
+// into LDS once behind one barrier, and its waves split the range's items into 8 equal contiguous
+// runs.  After that the waves never meet until the end: each streams its run through a private LDS
+// ring of D blocks that it alone fills and reads, so a block is ready when the wave's own load
+// counter says so (no barrier per block).
+//  * The balance: N = 25600 is 1600 units; in 128-column workgroups of one unit per wave that left 56
+//    of 256 CUs idle, with every wave 20 blocks long.  Here every CU works, a wave runs at most 18
+//    blocks, and a unit split between waves of one CU is added up through LDS after the loop, by the
+//    wave holding the unit's last block, over the waves' partial sums in the fixed order
+//    ((p_{n-1} + p_{n-2}) + ..) + p_0 -- no global traffic (units split across CUs, with their
+//    partials through memory and atomic counts, measured slower: at ~20 us a launch, each of their
+//    end-of-run round trips cost 1-3 us).
+//  * Scales and zeros: with G a multiple of 8 up to 40 and at most 8 units per CU, the CU's rows of
+//    both tables (contiguous in memory) go to LDS once with the activations (SZT); else each block
+//    loads its 16 rows' values into the ring (2-byte loads: ~16 cache lines each, as many as the
+//    block's weights).
+//  * The ring starts with two blocks and grows by one extra block per step up to D: issuing all D
+//    blocks before the first compute took ~12K cycles.  The two waves of a SIMD take turns at the
+//    higher issue priority: left to age order the older one ran ahead and the younger one finished
+//    alone.
 // The arithmetic is the streaming kernel's (w = round_16(fmaf(q, s, -z s)), 16x16x32 MFMA with the
 // activations as the A operand, lane group h carrying k = 64 h + 8 t of the block in k-step t).
 namespace wd {
-constexpr int NW = 8, ROWS = 16 * NW;                 // waves; weight rows per workgroup
+constexpr int NW = 8;                                 // waves per workgroup
 constexpr int B = 256;                                // k per block
 constexpr int WBYTES = 16 * B / 2;                    // a wave's nibbles per block (2 KB)
-constexpr int WSLOT = WBYTES + 256;                   // + its scale / zero words
+constexpr int SZW = 256;                              // a block's scale / zero words (no table)
 constexpr int MAXM = 8;
-constexpr int LOADS = 3;                              // ring loads per wave and block
+constexpr int TROWS = 128;                            // rows of the scale / zero table
+constexpr int SZT_MAX = 2 * TROWS * 40 * 2;           // 20 KB: G <= 40
 __host__ __device__ inline int64_t xrow(int64_t K) { return 2 * K + 16; } // padded activation row in LDS (bytes)
+inline int64_t lds_bytes(int64_t M, int64_t K, int D, bool szt)
+{
+    return M * xrow(K) + (int64_t)NW * D * (WBYTES + (szt ? 0 : SZW)) + (szt ? SZT_MAX : 0);
+}
 // The wave's 16 weight rows are 128 bytes each, lane (n, h) reading chunks 2 h and 2 h + 1 of row n:
 // chunk c of row r sits at c ^ dsw(r), row bits (3, 1, 2) -> chunk bits (0, 1, 2), a placement free of
-// bank conflicts under every ds_read_b128 lane grouping an in-bounds probe of the LDS allows (the
-// earlier c ^ ((r >> 1) & 7) conflicted two ways).
+// bank conflicts for gfx950's ds_read_b128 lane groups (the earlier c ^ ((r >> 1) & 7) conflicted
+// two ways).
 __device__ __forceinline__ int dsw(int r) { return ((r >> 3) & 1) | (r & 6); }
-inline int64_t lds_bytes(int64_t M, int64_t K, int D) { return M * xrow(K) + (int64_t)NW * D * WSLOT; }
+// run g of W over T items is [run_start(g), run_start(g + 1)); run_owner(t) is the run holding item t
+__host__ __device__ inline int64_t run_start(int64_t g, int64_t T, int64_t W) { return g * T / W; }
+__host__ __device__ inline int64_t run_owner(int64_t t, int64_t T, int64_t W) { return ((t + 1) * W + T - 1) / T - 1; }
 }  // namespace wd
 
-template <int XDT, int D>
+template <int XDT, int D, bool SZT>
 __global__ void __launch_bounds__(wd::NW * 64)
 gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
 {
     using namespace wd;
     using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
+    constexpr int WS = WBYTES + (SZT ? 0 : SZW);          // ring slot bytes
+    constexpr int LOADS = SZT ? 2 : 3;                   // ring loads per block
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nr = lane & 15, h = lane >> 4;
     const int nb = K / B, G = K / wa.gs, hg = wa.gs / 128;
     const int64_t wld = K / 2, xr = xrow(K);
-    const int wg_row0 = blockIdx.x * ROWS, row0 = wg_row0 + 16 * wave;
-    uint8_t *const ring = smem + (int64_t)M * xr + (int64_t)wave * D * WSLOT;
-    // the weights from the workgroup's first row: lane offsets stay below 128 rows (32 bits)
-    const uint8_t *const wq = wa.wq + (int64_t)wg_row0 * wld;
+    // the workgroup's units [ua, ub) (G = gridDim.x workgroups over the units), their I items, this
+    // wave's run [t0, t1) of them (absolute item numbers)
+    // (the runs of one workgroup in 32-bit arithmetic: I < 2^28 / NW, checked by the host)
+    const int64_t units = (N + 15) / 16;
+    const int64_t ua = run_start(blockIdx.x, units, gridDim.x), ub = run_start(blockIdx.x + 1, units, gridDim.x);
+    const int I = (int)((ub - ua) * nb);
+    auto wrun = [&](int w) { return w * I / NW; };                     // run start of wave w (relative)
+    auto wowner = [&](int t) { return ((t + 1) * NW + I - 1) / I - 1; };  // the wave holding relative item t
+    const int64_t t0 = ua * nb + wrun(wave), t1 = ua * nb + wrun(wave + 1);
+    uint8_t *const tab = smem + (int64_t)M * xr;                                  // [scale | zero][row][G]
+    uint8_t *const ring0 = tab + (SZT ? SZT_MAX : 0);
+    uint8_t *const ring = ring0 + (int64_t)wave * D * WS;
+    const int64_t trow0 = 16 * ua;                     // the table's first row
 
     // the activations: row m at m * xr, 1 KB per wave load (K % 512 == 0: whole loads per row)
     const int per_row = (int)(2 * (int64_t)K / 1024), nx = M * per_row;
@@ -1136,133 +1168,311 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
         __builtin_amdgcn_global_load_lds((glb_ptr)((const uint8_t *)x + (int64_t)m * ldx * 2 + c * 1024 + lane * 16),
                                          (lds_ptr)(smem + (int64_t)m * xr + c * 1024), 16, 0, 0);
     }
-    // a block's ring loads (past the end: the last block again, into a slot nobody reads)
-    uint32_t wo[2];
-#pragma unroll
-    for (int d = 0; d < 2; d++) {
-        const int r = 8 * d + lane / 8, pc = lane % 8;
-        wo[d] = (uint32_t)((min(row0 + r, N - 1) - wg_row0) * wld + ((pc ^ dsw(r)) << 4));
+    if constexpr (SZT) {
+        // TROWS G halves per array from row trow0, in 1 KB loads; lanes past the last row read the
+        // last 16 bytes instead (their columns are never stored; G % 8 == 0 keeps every load aligned)
+        const int tb = TROWS * G * 2, nl = (tb + 1023) / 1024;
+        const int64_t valid = min((int64_t)TROWS, (int64_t)N - trow0) * G * 2;
+        for (int i = wave; i < 2 * nl; i += NW) {
+            const int arr = i >= nl, j = i - arr * nl, off = j * 1024 + 16 * lane;
+            const uint8_t *src = (const uint8_t *)((arr ? wa.zero16 : wa.scale16) + trow0 * G);
+            if (off < tb)
+                __builtin_amdgcn_global_load_lds((glb_ptr)(src + min((int64_t)off, valid - 16)),
+                                                 (lds_ptr)(tab + arr * tb + j * 1024), 16, 0, 0);
+        }
     }
-    const bool szhi = (lane & 1) != 0;
-    const uint16_t *const szrow = (lane < 32 ? wa.scale16 : wa.zero16) + (int64_t)min(row0 + ((lane >> 1) & 15), N - 1) * G;
-    // blocks are issued in order; the group of half 2 b is kept as a running quotient gq and
-    // remainder gr of 2 b by hg on the scalar unit (no per-lane division)
-    int gq = 0, gr = 0;
-    auto issue = [&](int b, int slot) {
-        const int bc = min(b, nb - 1);
-        uint8_t *const sl = ring + slot * WSLOT;
-        const uint8_t *const wb = wq + (int64_t)bc * (B / 2);
+    // a block's ring loads: item t (past the end of the run: its last item again, into a slot nobody
+    // reads).  Weights: rows 8 d + L / 8 (d = 0, 1) of the unit, physical chunk L % 8, holding
+    // logical chunk pc ^ dsw(row); rows past N clamp to the last row.  Without the table, lane L also
+    // fetches array L >> 5 (scale, zero), row (L >> 1) & 15 and 128-k half L & 1 into word L.
+    // the next item to issue, as unit ic and block ikb (running: no division per block); past the end
+    // of the run the last item is issued again
+    int64_t ti = t0;
+    int64_t ic = t0 / nb;
+    int ikb = (int)(t0 - ic * nb);
+    int igq = 0, igr = 0;                              // (2 ikb) / hg and (2 ikb) % hg (no table)
+    if constexpr (!SZT) { igq = (2 * ikb) / hg; igr = (2 * ikb) % hg; }
+    // weights of unit ic: the unit's first row as the base, the lanes' row offsets (rows past N
+    // clamped) set again only when the unit changes
+    const uint8_t *ubase = nullptr;
+    uint32_t wo[2];
+    auto set_unit = [&] {
+        ubase = wa.wq + (16 * ic) * wld;
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const int r = 8 * d + (lane >> 3);
+            wo[d] = (uint32_t)((min(16 * ic + r, (int64_t)N - 1) - 16 * ic) * wld + (((lane & 7) ^ dsw(r)) << 4));
+        }
+    };
+    if (t0 < t1) set_unit();
+    auto issue = [&](int slot) {
+        uint8_t *const sl = ring + slot * WS;
+        const uint8_t *const wb = ubase + ikb * (B / 2);
 #pragma unroll
         for (int d = 0; d < 2; d++)
             __builtin_amdgcn_global_load_lds((glb_ptr)(wb + wo[d]), (lds_ptr)(sl + 1024 * d), 16, 0, 0);
-        const int g = min(gq + (szhi && gr + 1 >= hg ? 1 : 0), G - 1);   // group of the lane's 128-k half
-        __builtin_amdgcn_global_load_lds((glb_ptr)(szrow + g), (lds_ptr)(sl + WBYTES), 2, 0, 0);
-        gr += 2;
-        if (gr >= hg) { gr -= hg; gq++; }
-        if (gr >= hg) { gr -= hg; gq++; }
+        if constexpr (!SZT) {
+            const int64_t row = min(16 * ic + ((lane >> 1) & 15), (int64_t)N - 1);
+            const int g = min(igq + ((lane & 1) && igr + 1 >= hg ? 1 : 0), G - 1);
+            __builtin_amdgcn_global_load_lds((glb_ptr)((lane < 32 ? wa.scale16 : wa.zero16) + row * G + g),
+                                             (lds_ptr)(sl + WBYTES), 2, 0, 0);
+        }
+        if (++ti < t1) {
+            if (++ikb == nb) {
+                ikb = 0;
+                ic++;
+                igq = igr = 0;
+                set_unit();
+            } else if constexpr (!SZT) {
+                igr += 2;
+                if (igr >= hg) { igr -= hg; igq++; }
+                if (igr >= hg) { igr -= hg; igq++; }
+            }
+        }
     };
-#pragma unroll
-    for (int b = 0; b < D; b++) issue(b, b);
-    wait_vmcnt<LOADS * D>();            // this wave's activation loads (issued first) landed
+    // The ring starts with two blocks and grows by one extra block per step until D are in flight:
+    // issuing all D blocks before the first compute took ~12K cycles (~160 global->LDS loads per CU).
+    // Block b goes to slot b % D; before the wait of step j (for block j + 1) min(2 + 2 j, j + D) blocks
+    // are issued, min(j, D - 2) of them younger than block j + 1.
+    // (a wave with an empty run -- fewer items than waves -- loads no ring blocks at all)
+    const bool active = t0 < t1;
+    int nissued = 0;
+    auto issue_next = [&] { issue(nissued % D); nissued++; };
+    if (active) {
+        issue_next();
+        issue_next();
+        wait_vmcnt<LOADS * 2>();        // this wave's activation and table loads (issued first) landed
+    } else {
+        wait_vmcnt<0>();
+    }
     stage_barrier();                    // ... and every other wave's
 
     struct Ops { XV xf[8]; v4i wv[2]; float sc, sc4, zs; };
     const uint8_t *const xrow_p = smem + (int64_t)min(nr, M - 1) * xr;
-    auto read = [&](int b, int slot, Ops &o) {
-        const uint8_t *const sl = ring + slot * WSLOT;
+    // the next item to read, as unit rc and block rkb, and the table group of its 128-k half 0
+    // (running, as for the issues)
+    int64_t rc = t0 / nb;
+    int rkb = (int)(t0 - rc * nb);
+    int rgq = (2 * rkb) / hg, rgr = (2 * rkb) % hg;
+    auto read = [&](int slot, bool advance, Ops &o) {
+        const uint8_t *const sl = ring + slot * WS;
 #pragma unroll
-        for (int t = 0; t < 8; t++)
-            o.xf[t] = __builtin_bit_cast(XV, *(const v4i *)(xrow_p + ((int64_t)b * B + 64 * h + 8 * t) * 2));
+        for (int s = 0; s < 8; s++)
+            o.xf[s] = __builtin_bit_cast(XV, *(const v4i *)(xrow_p + ((int64_t)rkb * B + 64 * h + 8 * s) * 2));
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int c = 2 * h + i;
-            o.wv[i] = *(const v4i *)(sl + nr * (B / 2) + ((c ^ dsw(nr)) << 4));
+            const int cc = 2 * h + i;
+            o.wv[i] = *(const v4i *)(sl + nr * (B / 2) + ((cc ^ dsw(nr)) << 4));
         }
-        const int si = (nr << 1) | (h >> 1);
-        const uint32_t *sz = (const uint32_t *)(sl + WBYTES);
-        const float sv = f16_to_f32(sz[si]);
-        o.zs = -(f16_to_f32(sz[32 + si]) * sv);
+        float sv, zv;
+        if constexpr (SZT) {
+            const int row = (int)(16 * rc - trow0) + nr, g = rgq + ((h >> 1) && rgr + 1 >= hg ? 1 : 0);
+            const uint16_t *tb16 = (const uint16_t *)tab;
+            sv = f16_to_f32(tb16[row * G + g]);
+            zv = f16_to_f32(tb16[(TROWS + row) * G + g]);
+        } else {
+            const int si = (nr << 1) | (h >> 1);
+            const uint32_t *sz = (const uint32_t *)(sl + WBYTES);
+            sv = f16_to_f32(sz[si]);
+            zv = f16_to_f32(sz[32 + si]);
+        }
+        o.zs = -(zv * sv);
         o.sc = sv * kTwo24;                 // s 2^24 and s 2^20 (dq_pair_u4)
         o.sc4 = sv * kTwo20;
+        if (advance) {
+            if (++rkb == nb) {
+                rkb = 0;
+                rc++;
+                rgq = rgr = 0;
+            } else {
+                rgr += 2;
+                if (rgr >= hg) { rgr -= hg; rgq++; }
+                if (rgr >= hg) { rgr -= hg; rgq++; }
+            }
+        }
     };
     v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](const Ops &o) {
         XV wfs[8];
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const Nib4 v = nib_split((uint32_t)o.wv[t >> 2][t & 3]);
+        for (int s = 0; s < 8; s++) {
+            const Nib4 v = nib_split((uint32_t)o.wv[s >> 2][s & 3]);
             uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, o.sc, o.sc4, o.zs);
-            wfs[t] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+            wfs[s] = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
         }
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            if constexpr (XDT == PSQ_BF16) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.xf[t], wfs[t], acc, 0, 0, 0);
-            else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.xf[t], wfs[t], acc, 0, 0, 0);
+        for (int s = 0; s < 8; s++) {
+            if constexpr (XDT == PSQ_BF16) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.xf[s], wfs[s], acc, 0, 0, 0);
+            else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.xf[s], wfs[s], acc, 0, 0, 0);
         }
     };
-    // Pipeline: block b + 1 is read while block b computes; block b's slot is refilled once its
-    // registers have been used (after compute).  Block b + 1 has landed when at most D - 2 younger
-    // blocks of this wave are in flight.
-    Ops oa, ob;
-    wait_vmcnt<LOADS * (D - 1)>();
-    read(0, 0, oa);
-    int slot = 0;
-    auto step = [&](int b, const Ops &cur, Ops &nxt) {
-        const int nslot = slot == D - 1 ? 0 : slot + 1;
-        wait_vmcnt<LOADS * (D - 2)>();
-        read(b + 1 < nb ? b + 1 : b, nslot, nxt);
-        compute(cur);
-        issue(b + D, slot);
-        slot = nslot;
-    };
-    for (int b = 0; b < nb; b += 2) {
-        step(b, oa, ob);
-        if (b + 1 < nb) step(b + 1, ob, oa);
-    }
-    wait_vmcnt<0>();
-    // y[m][n] = round_out(acc + bias[n]); lane: n = row0 + nr, m = 4 h + v
-    const int n = row0 + nr;
-    if (n < N) {
+    // y[m][n] = round_out(v + bias[n]) for unit c; lane: n = 16 c + nr, m = 4 h + r
+    auto store = [&](int64_t c, v4f v) {
+        const int64_t n = 16 * c + nr;
+        if (n >= N) return;
         const float bb = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int m = 4 * h + v;
-            if (m < M) store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype, acc[v] + bb);
+        for (int r = 0; r < 4; r++) {
+            const int m = 4 * h + r;
+            if (m < M) store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype, v[r] + bb);
         }
+    };
+
+    // Pipeline: block t + 1 is read while block t computes; block t's slot is refilled once its
+    // registers have been used (after compute).  Block t + 1 has landed when at most D - 2 younger
+    // blocks of this wave are in flight.  At the end of a unit (or of the run) the segment's sum is
+    // stored (a whole unit), kept (a partial first segment) or left in acc (a partial last one).
+    Ops oa, ob;
+    int slot = 0;
+    v4f acc0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    bool first_partial = false, last_partial = false;
+    if (t0 < t1) {
+        wait_vmcnt<LOADS * 1>();
+        read(0, true, oa);
     }
+    // this wave's loads of block j + 1 landed: min(j, D - 2) younger blocks may be in flight
+    auto wait_next = [&](int j) {
+        switch (min(j, D - 2)) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<LOADS * 1>(); break;
+        case 2: wait_vmcnt<LOADS * 2>(); break;
+        case 3: wait_vmcnt<LOADS * 3>(); break;
+        case 4: wait_vmcnt<LOADS * 4>(); break;
+        case 5: wait_vmcnt<LOADS * 5>(); break;
+        default: wait_vmcnt<LOADS * 6>(); break;
+        }
+    };
+    // the item computed, as unit cc and block ckb; whether the current segment began at a unit's start
+    int64_t cc = t0 / nb;
+    int ckb = (int)(t0 - cc * nb);
+    bool seg_whole_start = ckb == 0;
+    auto step = [&](int64_t t, const Ops &cur, Ops &nxt) {
+        const int nslot = slot == D - 1 ? 0 : slot + 1;
+        const int j = (int)(t - t0);
+        // the two waves of a SIMD (w, w + 4) take turns at the higher issue priority, two blocks each:
+        // left to age order the older wave ran ahead and the younger one finished alone
+        if (((j >> 1) ^ (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+        wait_next(j);
+        read(nslot, t + 2 < t1, nxt);                  // item t + 1 (past the end: read again, unused)
+        compute(cur);
+        issue_next();                                  // block j + D at the latest: slot j % D is free
+        if (nissued <= j + D) issue_next();            // the ramp
+        slot = nslot;
+        const bool unit_end = ckb == nb - 1;
+        if (t == t1 - 1 || unit_end) {
+            if (seg_whole_start && unit_end) {
+                store(cc, acc);
+                acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            } else if (t != t1 - 1) {                  // a partial segment that ends before the run: the first
+                acc0 = acc;
+                first_partial = true;
+                acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            } else {
+                last_partial = true;                   // the run's last segment (or its only one)
+            }
+            seg_whole_start = true;
+        }
+        if (++ckb == nb) {
+            ckb = 0;
+            cc++;
+        }
+    };
+    for (int64_t t = t0; t < t1; t += 2) {
+        step(t, oa, ob);
+        if (t + 1 < t1) step(t + 1, ob, oa);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    wait_vmcnt<0>();                                    // the re-issued tail loads, before any partial traffic
+
+    // ---- units split between this CU's waves: each wave's partial first segment (unit t0 / nb) and
+    // partial last one (unit (t1 - 1) / nb) go to LDS slot 2 w + (0: the run's first unit, 1: else),
+    // 1 KB in the lanes' order, once every wave is done with its ring; the wave holding a unit's last
+    // block then adds the unit up in wave order (its own partial from registers) and stores it.
+    __syncthreads();
+    float *const red = (float *)ring0;
+    // units relative to ua (int): the run's first and last, and the first unit of wave w's run
+    const int rf = wrun(wave) / nb, rl = t0 < t1 ? (wrun(wave + 1) - 1) / nb : rf;
+    auto slot_of = [&](int w, int c) { return 2 * w + (wrun(w) / nb == c ? 0 : 1); };
+    auto put = [&](int c, v4f v) { *(v4f *)(red + (slot_of(wave, c) * 64 + lane) * 4) = v; };
+    if (first_partial) put(rf, acc0);
+    if (last_partial) put(rl, acc);
+    __syncthreads();
+    auto addup = [&](int c, v4f v) {
+        const int lf = wowner(c * nb), ll = wowner(c * nb + nb - 1);
+        v4f sum = v;                                   // this wave holds the unit's last block: p_{n-1}
+        for (int w = ll - 1; w >= lf; w--)             // (waves with empty runs hold no partial)
+            if (wrun(w + 1) > wrun(w)) sum = sum + *(const v4f *)(red + (slot_of(w, c) * 64 + lane) * 4);
+        store(ua + c, sum);
+    };
+    // a partial segment ending at its unit's last block: the first one (always), or the only one
+    if (first_partial) addup(rf, acc0);
+    if (last_partial && wrun(wave + 1) % nb == 0) addup(rl, acc);
 }
 
 // The decode kernel's ring depth for M rows of K (0: the shape does not fit).
-int decode_depth(int64_t M, int64_t K)
+int decode_depth(int64_t M, int64_t K, bool szt)
 {
-    for (int d : {8, 6, 4})
-        if (wd::lds_bytes(M, K, d) <= 163840) return d;
+    for (int d : {8, 6, 4, 3})
+        if (wd::lds_bytes(M, K, d, szt) <= 163840) return d;
     return 0;
 }
 
-template <int XDT, int D>
+// Launch plan of the decode kernel: G workgroups (one per CU while there are units) and the scale /
+// zero form (the table when G is a multiple of 8 up to 40, the tables are 16-byte aligned and a
+// workgroup's units are at most TROWS / 16).
+struct DecodePlan {
+    int64_t G = 0;              // workgroups
+    bool szt = false;
+    int depth = 0;
+};
+DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int gs, const void *scale, const void *zero, int cus)
+{
+    DecodePlan p;
+    const int64_t units = (N + 15) / 16, G = K / gs;
+    p.G = std::min<int64_t>(units, cus);
+    const int64_t upw = (units + p.G - 1) / p.G;                 // units per workgroup, at most
+    if (upw * (K / wd::B) * wd::NW >= (1LL << 31)) p.G = 0;      // a workgroup's runs need 32-bit item numbers
+    p.szt = G % 8 == 0 && G <= 40 && upw <= wd::TROWS / 16 && ((uintptr_t)scale & 15) == 0 &&
+            ((uintptr_t)zero & 15) == 0;
+    p.depth = decode_depth(M, K, p.szt);
+    if (p.depth == 0 && p.szt) {
+        p.szt = false;
+        p.depth = decode_depth(M, K, false);
+    }
+    return p;
+}
+
+template <int XDT, int D, bool SZT>
 int launch_decode_d(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
                     const char *name)
 {
-    auto kern = gemm_w4_decode<XDT, D>;
-    const int lds = (int)wd::lds_bytes(M, K, D);
+    auto kern = gemm_w4_decode<XDT, D, SZT>;
+    const int lds = (int)wd::lds_bytes(M, K, D, SZT);
     if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
         return set_error(PSQ_E_DEVICE, "%s: cannot reserve LDS", name);
-    const dim3 grid((unsigned)((N + wd::ROWS - 1) / wd::ROWS)), block(wd::NW * 64);
+    const dim3 grid((unsigned)wa.sk), block(wd::NW * 64);
     kern<<<grid, block, lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
     return check_launch(name);
 }
 
 template <int XDT>
-int launch_decode(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, hipStream_t st,
-                  const char *name)
+int launch_decode(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, WArgs wa, const DecodePlan &p,
+                  hipStream_t st, const char *name)
 {
-    const int d = decode_depth(M, K);
-    if (d == 8) return launch_decode_d<XDT, 8>(x, ldx, M, N, K, wa, st, name);
-    if (d == 6) return launch_decode_d<XDT, 6>(x, ldx, M, N, K, wa, st, name);
-    return launch_decode_d<XDT, 4>(x, ldx, M, N, K, wa, st, name);
+    wa.sk = (int)p.G;
+    auto go = [&](auto szc) {
+        constexpr bool S = decltype(szc)::value;
+        switch (p.depth) {
+        case 8: return launch_decode_d<XDT, 8, S>(x, ldx, M, N, K, wa, st, name);
+        case 6: return launch_decode_d<XDT, 6, S>(x, ldx, M, N, K, wa, st, name);
+        case 4: return launch_decode_d<XDT, 4, S>(x, ldx, M, N, K, wa, st, name);
+        default: return launch_decode_d<XDT, 3, S>(x, ldx, M, N, K, wa, st, name);
+        }
+    };
+    return p.szt ? go(std::true_type{}) : go(std::false_type{});
 }
 
 template <int XDT, int MT, int SZM>
@@ -1421,7 +1631,7 @@ enum class Path { Decode, Stream, Skinny, Tiled };
 
 Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
 {
-    if (wk == W_UINT4 && M <= wd::MAXM && gs % 128 == 0 && K % 512 == 0 && decode_depth(M, K) > 0 &&
+    if (wk == W_UINT4 && M <= wd::MAXM && gs % 128 == 0 && K % 512 == 0 && decode_depth(M, K, false) > 0 &&
         ldx <= (1LL << 22))
         return Path::Decode;
     if (wk == W_UINT4 && M <= SKINNY_MAX_M && gs % 128 == 0 && K % ws::STEP == 0 && ldx <= (1LL << 22))
@@ -1433,7 +1643,9 @@ Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
 // Workspace bytes of a call (0: no split); the split needs a device, else 0.
 int64_t workspace_bytes(int wk, int64_t ldx, int64_t M, int64_t N, int64_t K, int gs)
 {
-    if (M <= 0 || N <= 0 || K <= 0 || choose_path(wk, ldx, M, K, gs) != Path::Tiled) return 0;
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const Path path = choose_path(wk, ldx, M, K, gs);
+    if (path != Path::Tiled) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     return plan_tiled(M, N, K, cu_count(dev), true).ws_bytes;
@@ -1447,10 +1659,16 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
            void *workspace, int64_t ws_bytes, hipStream_t st, const char *name)
 {
     const uint16_t *xp = (const uint16_t *)x;
-    const Path path = choose_path(WK, ldx, M, K, wa.gs);
-    if (path == Path::Decode)
-        return x_dtype == PSQ_BF16 ? launch_decode<PSQ_BF16>(xp, ldx, M, N, K, wa, st, name)
-                                   : launch_decode<PSQ_F16>(xp, ldx, M, N, K, wa, st, name);
+    Path path = choose_path(WK, ldx, M, K, wa.gs);
+    if (path == Path::Decode) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
+        const DecodePlan plan = plan_decode(M, N, K, wa.gs, wa.scale16, wa.zero16, cu_count(dev));
+        if (plan.G > 0)
+            return x_dtype == PSQ_BF16 ? launch_decode<PSQ_BF16>(xp, ldx, M, N, K, wa, plan, st, name)
+                                       : launch_decode<PSQ_F16>(xp, ldx, M, N, K, wa, plan, st, name);
+        path = Path::Stream;   // too many items per workgroup for 32-bit runs: the streaming kernel takes it
+    }
     if (path == Path::Stream)
         return x_dtype == PSQ_BF16 ? launch_stream<PSQ_BF16>(xp, ldx, M, N, K, wa, st, name)
                                    : launch_stream<PSQ_F16>(xp, ldx, M, N, K, wa, st, name);

@@ -457,11 +457,16 @@ def test_gemm_w4a16_unsplit_entry_point(gpu):
 @pytest.mark.parametrize("M,N,K,gs", [(1, 25600, 5120, 128), (2, 2600, 5120, 128), (3, 389, 1024, 256),
                                       (4, 1000, 3072, 128), (1, 130, 25600, 128), (4, 256, 512, 512),
                                       (5, 777, 5120, 128), (8, 25600, 5120, 128), (6, 300, 12800, 256),
-                                      (7, 129, 1024, 128)])
+                                      (7, 129, 1024, 128), (3, 25600, 6144, 128)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemm_w4a16_decode(gpu, M, N, K, gs, xdt):
     """M <= 8 with K % 512 == 0 (the activations fitting in LDS) runs the barrier-free decode kernel
-    (activations in LDS, a private weight ring per wave); same bar as the other weight-only paths."""
+    (activations in LDS, a private weight ring per wave); same bar as the other weight-only paths.
+    Each CU takes a range of 16-column units whose items its 8 waves split evenly, and a unit split
+    between waves is added up through LDS in a fixed order: N = 25600 (7 units on some CUs), 2600
+    (one unit per CU over 8 waves), 389 x 1024 and 129 x 1024 (fewer items than waves: empty runs),
+    with the scale / zero tables in LDS or, at K = 6144 (G = 48 > 40) and K = 12800, per-block scale
+    loads.  Repeated calls are bit-identical."""
     from powershard_amd import ops
     x = heavy_rows(M, K, seed=110 + M, outlier_frac=0, dtype=xdt)
     w = torch.randn(N, K, generator=seeded(111)) * 0.02
@@ -469,6 +474,10 @@ def test_gemm_w4a16_decode(gpu, M, N, K, gs, xdt):
     b = (torch.randn(N, generator=seeded(112)) * 0.01).to(xdt)
     args = (x.to(gpu), wq.to(gpu), s.to(gpu), z.to(gpu), gs, b.to(gpu))
     y32 = ops.gemm_w4a16(*args, out_dtype=torch.float32)
+    for _ in range(3):
+        again = ops.gemm_w4a16(*args, out_dtype=torch.float32)
+        assert torch.equal(again.view(torch.int32), y32.view(torch.int32)), "decode result changed between calls"
     yb = ops.gemm_w4a16(*args, out_dtype=torch.bfloat16)
     wd = oracle.dequant_uint4(wq, s, z, gs, out_dtype=xdt)
     assert_fp32_path(y32, yb, oracle.gemm_wonly(x, wd, None, b, out_dtype=torch.float32), f"w4a16 decode {M}x{N}x{K}")
+
