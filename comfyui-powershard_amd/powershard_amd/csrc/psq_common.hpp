@@ -167,6 +167,7 @@ enum : int {
     DPP_QUAD_XOR3 = 0x1B,        // quad_perm [3,2,1,0]
     DPP_ROW_MIRROR = 0x140,      // lane ^ 15 within a row of 16
     DPP_ROW_HALF_MIRROR = 0x141, // lane ^ 7 within a half row of 8
+    DPP_ROW_ROR4 = 0x124,        // lane (l + 4) mod 16 within a row of 16
     DPP_ROW_ROR8 = 0x128         // lane ^ 8 within a row of 16
 };
 
@@ -227,6 +228,18 @@ __device__ __forceinline__ float radix4_lanes_rev(float x)
 {
     float t = x + lane_xor<L, 1>(x);
     float s = t + lane_xor<L, 2>(t);
+    return __builtin_fmaf(-2.0f, x, s);
+}
+
+// The reversed stage over lane bits 2-3 for a digit stored with its bits swapped (digit bit 0 on lane
+// bit 3, digit bit 1 on lane bit 2).  The pair partner (digit ^ 1) is then lane ^ 8, and the other
+// pair's sum, the same value on both of its lanes, sits at lane + 4 mod 16: two DPP adds (row_ror:8,
+// row_ror:4) and the fma, where the unswapped digit needs a DPP move for lane ^ 4 as well.  Same
+// operations in the same order as radix4_lanes_rev<4>, so the same bits.
+__device__ __forceinline__ float radix4_lanes_rev_sw4(float x)
+{
+    float t = x + dpp<DPP_ROW_ROR8>(x);
+    float s = t + dpp<DPP_ROW_ROR4>(t);
     return __builtin_fmaf(-2.0f, x, s);
 }
 

@@ -14,10 +14,10 @@
 // consecutive elements (32 bytes of bf16 in, 16 bytes of codes out; both fully coalesced), one
 // chunk per 1024 threads of the row.  Base-4
 // digits 0 and 1 of the element index live inside a thread, digit 2 on lane bits 0-1 (DPP quad
-// permutes), digit 3 on lane bits 2-3 (DPP row mirrors/rotates), digit 4 on lane bits 4-5
-// (cross-lane shuffle; g = 1024 only).  The lane stages of digits 2 and 3 leave their outputs in
-// reversed digit order (each lane keeps the output its own input enters with -2), so a thread
-// stores its results at the chunk of lane t ^ rev_lanes: same values, one exchange fewer per
+// permutes), digit 3 on lane bits 2-3 with its two bits swapped (DPP row rotates), digit 4 on lane
+// bits 4-5 (cross-lane shuffle; g = 1024 only).  The lane stages of digits 2 and 3 leave their
+// outputs in reversed digit order (each lane keeps the output its own input enters with -2), so a
+// thread stores its results at the chunk of lane t ^ rev_lanes: same values, one exchange fewer per
 // stage.  The row's absmax is reduced across the wave with DPP and row swaps and across waves
 // through LDS.  2 bytes read + 1 byte written per element (+4 bytes per row).
 #include "psq_common.hpp"
@@ -81,19 +81,35 @@ __device__ __forceinline__ uint32_t wave_max_bits(uint32_t u)
 // integers), then + 1.5 * 2^23, which rounds to the nearest integer (ties to even) and leaves the
 // code's two's complement in the low byte of the sum.  A NaN clamps to -127, as fmax(NaN, -127)
 // does in the rounding-first order.
-__device__ __forceinline__ uint32_t i8_code_bits(float u)
+constexpr float kRoundMagic = 12582912.0f;
+
+__device__ __forceinline__ float i8_clamp(float u) { return __builtin_fminf(__builtin_fmaxf(u, -127.0f), 127.0f); }
+
+// Four codes packed into one word by the adds that round them: the first add writes the whole word
+// (its low byte is code 0), the other three are v_add_f32 with an SDWA destination, which writes
+// the low byte of the sum into byte B of the word and keeps the other bytes.  No separate pack.
+template <int B>
+__device__ __forceinline__ void add_into_byte(uint32_t &w, float u, float magic)
 {
-    u = __builtin_fminf(__builtin_fmaxf(u, -127.0f), 127.0f);
-    return __float_as_uint(u + 12582912.0f);
+    static_assert(B >= 1 && B <= 3, "byte 1-3");
+    if constexpr (B == 1)
+        asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(w) : "v"(u), "v"(magic));
+    else if constexpr (B == 2)
+        asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(w) : "v"(u), "v"(magic));
+    else
+        asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(w) : "v"(u), "v"(magic));
 }
 
-// Low bytes of four words packed into one (v_perm_b32: byte selectors 0-3 pick from the second
-// operand, 4-7 from the first, 12 gives zero).
-__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3)
+__device__ __forceinline__ uint32_t i8_codes4(float u0, float u1, float u2, float u3, float magic)
 {
-    const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);
-    const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
-    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    uint32_t w = __float_as_uint(i8_clamp(u0) + magic);
+    add_into_byte<1>(w, i8_clamp(u1), magic);
+    add_into_byte<2>(w, i8_clamp(u2), magic);
+    add_into_byte<3>(w, i8_clamp(u3), magic);
+    return w;
 }
 
 // Unnormalized transform of the 16 values of this thread (in-thread digits) and of the
@@ -101,6 +117,16 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uin
 // reversed (radix4_lanes_rev): the thread's 16 results belong to the chunk of thread t ^ rev_lanes.
 template <int ROTK>
 constexpr int rev_lanes() { return (ROTK >= 3 ? 3 : 0) | (ROTK >= 4 ? 12 : 0); }
+
+// Chunk (within its wave's 64) that lane t loads: lane bits 2 and 3 swapped when digit 3 lives on
+// them (see radix4_lanes_rev_sw4), so the chunk's digit-3 bit 0 sits on lane bit 3.  The wave's
+// loads and stores cover the same 2 KB and 1 KB as in lane order.
+template <int ROTK>
+__device__ __forceinline__ int lane_chunk(int t)
+{
+    if constexpr (ROTK >= 4) return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1);
+    else return t;
+}
 
 template <int ROTK>
 __device__ __forceinline__ void rotate16(float (&v)[16])
@@ -119,7 +145,7 @@ __device__ __forceinline__ void rotate16(float (&v)[16])
     }
     if constexpr (ROTK >= 4) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = radix4_lanes_rev<4>(v[j]);
+        for (int j = 0; j < 16; j++) v[j] = radix4_lanes_rev_sw4(v[j]);
     }
     if constexpr (ROTK >= 5) {
 #pragma unroll
@@ -129,23 +155,24 @@ __device__ __forceinline__ void rotate16(float (&v)[16])
 
 // A workgroup quantizes R consecutive rows side by side (all their loads issued up front, one
 // shared barrier for the absmax reductions).  Thread t owns P chunks of 16 consecutive elements
-// of each row: chunk c = elements [(c T + t) 16, +16), T = blockDim.x (a multiple of 64), so
-// every wave covers 1024 consecutive elements per chunk and rotation groups (at most 1024,
-// dividing K) never straddle waves.
-template <int DT, int ROTK, bool FP8, int P, int R>
+// of each row: chunk c = elements [(c T + lane_chunk(t)) 16, +16), T = blockDim.x (a multiple of
+// 64), so every wave covers 1024 consecutive elements per chunk and rotation groups (at most 1024,
+// dividing K) never straddle waves.  TAIL: some chunk lies past K (P T 16 > K); without it every
+// load and store is unconditional.
+template <int DT, int ROTK, bool FP8, int P, int R, bool TAIL>
 __global__ void __launch_bounds__(kMaxThreads)
 quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
                      const float *__restrict__ static_scale, uint8_t *__restrict__ q, int64_t ldq,
                      float *__restrict__ scale)
 {
     __shared__ uint32_t wave_amax[R][kMaxThreads / 64];
-    const int t = threadIdx.x, T = blockDim.x;
+    const int t = threadIdx.x, T = blockDim.x, lc = lane_chunk<ROTK>(t);
     const int row0 = blockIdx.x * R;
     constexpr float LIM = FP8 ? 448.0f : 127.0f;
     const float post = ROTK ? __builtin_ldexpf(1.0f, -ROTK) : 1.0f;
     bool act[P];
 #pragma unroll
-    for (int c = 0; c < P; c++) act[c] = (c * T + t) * kElemsPerThread < K;
+    for (int c = 0; c < P; c++) act[c] = !TAIL || (c * T + lc) * kElemsPerThread < K;
 
     // The activations are read once, non-temporally: streamed through with normal loads they evict
     // the codes this kernel writes, and the weights, from the 256 MB memory-side cache just before
@@ -155,7 +182,7 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
 #pragma unroll
     for (int rr = 0; rr < R; rr++) {
         const int row = min(row0 + rr, M - 1);
-        const uint16_t *src = x + (int64_t)row * ldx + (int64_t)t * kElemsPerThread;
+        const uint16_t *src = x + (int64_t)row * ldx + (int64_t)lc * kElemsPerThread;
 #pragma unroll
         for (int c = 0; c < P; c++) {
             v4i raw[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
@@ -171,21 +198,20 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
 #pragma unroll
         for (int c = 0; c < P; c++) rotate16<ROTK>(v[rr][c]);
 
-    float r[R], s[R];
+    // r multiplies the transformed values; the row scale s is only stored (by thread 0), so its
+    // division runs in wave 0 alone
+    float r[R], amax[R];
     if (static_scale) {
 #pragma unroll
-        for (int rr = 0; rr < R; rr++) {
-            s[rr] = *static_scale;
-            r[rr] = (1.0f / s[rr]) * post;
-        }
+        for (int rr = 0; rr < R; rr++) r[rr] = (1.0f / *static_scale) * post;
     } else {
         const int nw = T >> 6;
 #pragma unroll
         for (int rr = 0; rr < R; rr++) {
-            float amax = absmax16(v[rr][0]);
+            float m = absmax16(v[rr][0]);
 #pragma unroll
-            for (int c = 1; c < P; c++) amax = __builtin_elementwise_maximum(amax, absmax16(v[rr][c]));
-            const uint32_t bits = wave_max_bits(__float_as_uint(amax));
+            for (int c = 1; c < P; c++) m = __builtin_elementwise_maximum(m, absmax16(v[rr][c]));
+            const uint32_t bits = wave_max_bits(__float_as_uint(m));
             if ((t & 63) == 0) wave_amax[rr][t >> 6] = bits;
         }
         __syncthreads();
@@ -193,45 +219,37 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
         for (int rr = 0; rr < R; rr++) {
             uint32_t bits = wave_amax[rr][0];
             for (int w = 1; w < nw; w++) bits = max(bits, wave_amax[rr][w]);
-            const float amax = __uint_as_float(bits);
-            if (amax == 0.0f) {
-                s[rr] = 1.0f;
-                r[rr] = 1.0f;
-            } else {
-                r[rr] = LIM / amax;
-                s[rr] = (amax / LIM) * post;
-            }
+            amax[rr] = __uint_as_float(bits);
+            r[rr] = amax[rr] == 0.0f ? 1.0f : LIM / amax[rr];
         }
     }
 #pragma unroll
     for (int rr = 0; rr < R; rr++) {
         const int row = row0 + rr;
         if (row >= M) break;
-        if (t == 0) scale[row] = s[rr];
+        if (t == 0)
+            scale[row] = static_scale ? *static_scale : amax[rr] == 0.0f ? 1.0f : (amax[rr] / LIM) * post;
 #pragma unroll
         for (int c = 0; c < P; c++) {
             if (!act[c]) continue;
             uint32_t packed[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
+                const float *u = &v[rr][c][4 * i];
                 if constexpr (FP8) {
                     // gfx950's v_cvt_pk_fp8_f32 is the OCP e4m3fn encode with round to nearest
                     // even (subnormals included); the clamp keeps it off the overflow path and, as
                     // in the int8 codes, takes a NaN product to the lower bound
-                    float u[4];
+                    float uc[4];
 #pragma unroll
-                    for (int b = 0; b < 4; b++)
-                        u[b] = __builtin_fminf(__builtin_fmaxf(v[rr][c][4 * i + b] * r[rr], -448.0f), 448.0f);
-                    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(u[0], u[1], 0, false);
-                    packed[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(u[2], u[3], lo, true);
+                    for (int b = 0; b < 4; b++) uc[b] = __builtin_fminf(__builtin_fmaxf(u[b] * r[rr], -448.0f), 448.0f);
+                    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(uc[0], uc[1], 0, false);
+                    packed[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(uc[2], uc[3], lo, true);
                 } else {
-                    uint32_t cb[4];
-#pragma unroll
-                    for (int b = 0; b < 4; b++) cb[b] = i8_code_bits(v[rr][c][4 * i + b] * r[rr]);
-                    packed[i] = pack_low_bytes(cb[0], cb[1], cb[2], cb[3]);
+                    packed[i] = i8_codes4(u[0] * r[rr], u[1] * r[rr], u[2] * r[rr], u[3] * r[rr], kRoundMagic);
                 }
             }
-            *(v4i *)(q + (int64_t)row * ldq + (int64_t)(c * T + (t ^ rev_lanes<ROTK>())) * kElemsPerThread) =
+            *(v4i *)(q + (int64_t)row * ldq + (int64_t)(c * T + (lc ^ rev_lanes<ROTK>())) * kElemsPerThread) =
                 v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
         }
     }
@@ -244,18 +262,18 @@ template <int DT, int ROTK, int OUT, int P>
 __global__ void __launch_bounds__(kMaxThreads)
 rotate_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int K, void *__restrict__ y, int64_t ldy)
 {
-    const int t = threadIdx.x, T = blockDim.x, row = blockIdx.x;
+    const int t = threadIdx.x, T = blockDim.x, row = blockIdx.x, lc = lane_chunk<ROTK>(t);
     const float post = ROTK ? __builtin_ldexpf(1.0f, -ROTK) : 1.0f;
-    const uint16_t *src = x + (int64_t)row * ldx + (int64_t)t * kElemsPerThread;
+    const uint16_t *src = x + (int64_t)row * ldx + (int64_t)lc * kElemsPerThread;
 #pragma unroll
     for (int c = 0; c < P; c++) {
-        if ((c * T + t) * kElemsPerThread >= K) break;
+        if ((c * T + lc) * kElemsPerThread >= K) break;
         const int64_t off = (int64_t)c * T * kElemsPerThread;
         v4i raw[2] = {*(const v4i *)(src + off), *(const v4i *)(src + off + 8)};
         float v[16];
         to_f32<DT>(raw, v);
         rotate16<ROTK>(v);
-        const int64_t e0 = (int64_t)row * ldy + (int64_t)(c * T + (t ^ rev_lanes<ROTK>())) * kElemsPerThread;
+        const int64_t e0 = (int64_t)row * ldy + (int64_t)(c * T + (lc ^ rev_lanes<ROTK>())) * kElemsPerThread;
         if constexpr (OUT == PSQ_F32) {
             float *o = (float *)y + e0;
 #pragma unroll
@@ -299,16 +317,16 @@ int launch_rotate(const void *x, int64_t M, int64_t K, int64_t ldx, int rotk, vo
     return launch_rotate_p<DT, OUT, 1>(xp, M, K, ldx, rotk, threads, y, ldy, st);
 }
 
-template <int DT, bool FP8, int P, int R>
+template <int DT, bool FP8, int P, int R, bool TAIL>
 int launch_quant_p(const uint16_t *xp, int64_t M, int64_t K, int64_t ldx, int rotk, int threads,
                    const float *static_scale, uint8_t *q, int64_t ldq, float *scale, hipStream_t st)
 {
     const dim3 grid((unsigned)((M + R - 1) / R)), block(threads);
     switch (rotk) {
-#define PSQ_CASE(RK)                                                                           \
-    case RK:                                                                                   \
-        quantize_rows_kernel<DT, RK, FP8, P, R><<<grid, block, 0, st>>>(xp, ldx, (int)M, (int)K, \
-                                                                        static_scale, q, ldq, scale); \
+#define PSQ_CASE(RK)                                                                                \
+    case RK:                                                                                        \
+        quantize_rows_kernel<DT, RK, FP8, P, R, TAIL><<<grid, block, 0, st>>>(xp, ldx, (int)M, (int)K, \
+                                                                              static_scale, q, ldq, scale); \
         break;
         PSQ_CASE(0) PSQ_CASE(1) PSQ_CASE(2) PSQ_CASE(3) PSQ_CASE(4) PSQ_CASE(5)
 #undef PSQ_CASE
@@ -330,8 +348,12 @@ int launch_quant(const void *x, int64_t M, int64_t K, int64_t ldx, int rotk,
     const int P = chunks16 <= 512 ? 1 : 2;
     const int threads = (int)((chunks16 + P - 1) / P + 63) / 64 * 64;
     const uint16_t *xp = (const uint16_t *)x;
-    if (P == 2) return launch_quant_p<DT, FP8, 2, 1>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st);
-    return launch_quant_p<DT, FP8, 1, 1>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st);
+    const bool tail = (int64_t)P * threads * kElemsPerThread != K;
+    if (P == 2)
+        return tail ? launch_quant_p<DT, FP8, 2, 1, true>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st)
+                    : launch_quant_p<DT, FP8, 2, 1, false>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st);
+    return tail ? launch_quant_p<DT, FP8, 1, 1, true>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st)
+                : launch_quant_p<DT, FP8, 1, 1, false>(xp, M, K, ldx, rotk, threads, static_scale, q, ldq, scale, st);
 }
 
 // rot_group 0 (rotk 0) or a power of 4 in [4, 1024] dividing K (rotk = its base-4 log)
