@@ -56,8 +56,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--extras", default="", help="comma-separated subset of the extra workloads to run "
-                    "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, h3_mlp_silu_gate, shard_m4095, wan14b_stack); "
-                    "default all")
+                    "(int4_w4a16, fp8, w8a16, wan_ffn_gelu, h3_mlp_silu_gate, shard_m4095, wan14b_stack; "
+                    "gemm_i8_8wave, the int8 GEMM's 8-wave comparison schedule, only when named); default all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
                     help="target time of each timed CPU baseline sample (about ten samples in all)")
@@ -687,6 +687,48 @@ def extra_w8a16(args):
     return res
 
 
+def extra_8wave(args):
+    """The int8 GEMM's 8-wave comparison schedule (psq_gemm_i8_8wave: two waves per SIMD, 128 x 64
+    wave tiles, the same ring) against the kernel in use (psq_gemm_i8), bf16 output with a bias, on
+    the c1 and c4-down GEMMs: launches of the two alternate in rounds (10 untimed + 20 timed each,
+    three rounds, the fastest round kept), outputs compared bit for bit.  Run only when named."""
+    import ctypes
+    import torch
+    from powershard_amd import _native
+    lib = _native.lib()
+    res = {}
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    for tag, (M, N, K) in (("c1_ffn_up", (32760, 13824, 5120)), ("c4_ffn_down", (32760, 5120, 13824))):
+        g = gen(8100 + N)
+        a = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+        w = torch.randint(-127, 128, (N, K), generator=g, device="cuda", dtype=torch.int8)
+        sa = torch.rand(M, generator=g, device="cuda") * 0.01 + 1e-3
+        sw = torch.rand(N, generator=g, device="cuda") * 1e-3 + 1e-5
+        b = (torch.randn(N, generator=g, device="cuda") * 0.1).to(torch.bfloat16)
+        ys = {n: torch.empty(M, N, dtype=torch.bfloat16, device="cuda") for n in ("gemm_i8", "gemm_i8_8wave")}
+        fns = {"gemm_i8": lib.psq_gemm_i8, "gemm_i8_8wave": lib.psq_gemm_i8_8wave}
+
+        def run(n):
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            rc = fns[n](P(a), K, P(sa), P(w), K, P(sw), P(b), _native.BF16, P(ys[n]), _native.BF16, N, M, N, K, st)
+            if rc != 0:
+                raise RuntimeError(_native.last_error())
+        times = {n: [] for n in fns}
+        for _ in range(3):
+            for n in fns:
+                times[n].append(untimed_kernel_ms(lambda: run(n), 20, 10))
+        same = torch.equal(ys["gemm_i8"].view(torch.int16), ys["gemm_i8_8wave"].view(torch.int16))
+        ops = 2.0 * M * N * K
+        res[tag] = dict(M=M, N=N, K=K, bit_identical=same,
+                        **{f"{n}_ms": min(t) for n, t in times.items()},
+                        **{f"{n}_rounds_ms": [round(v, 4) for v in t] for n, t in times.items()},
+                        **{f"{n}_tops": ops / (min(t) * 1e-3) / 1e12 for n, t in times.items()})
+        log(f"[bench] 8-wave {tag}: gemm_i8 {min(times['gemm_i8']):.3f} ms, 8-wave {min(times['gemm_i8_8wave']):.3f} "
+            f"ms, bit-identical {same}")
+        del a, w, ys
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -720,8 +762,10 @@ def main():
         for name, fn in (("int4_w4a16", extra_int4), ("fp8", extra_fp8), ("w8a16", extra_w8a16),
                          ("wan_ffn_gelu", extra_ffn), ("h3_mlp_silu_gate", extra_h3_mlp),
                          ("shard_m4095", extra_shard),
-                         ("wan14b_stack", extra_wan_stack)):
+                         ("wan14b_stack", extra_wan_stack), ("gemm_i8_8wave", extra_8wave)):
             if args.extras and name not in args.extras.split(","):
+                continue
+            if name == "gemm_i8_8wave" and not args.extras:   # a comparison, run only when named
                 continue
             try:
                 extra[name] = fn(args)

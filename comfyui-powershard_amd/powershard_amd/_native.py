@@ -31,6 +31,7 @@ SIGNATURES = {
     "psq_gemm_i8": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_i8_act": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_i8_i32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P]),
+    "psq_gemm_i8_8wave": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_fp8": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_fp8_e5m2w": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
     "psq_gemm_fp8_act": (_I, [_P, _I64, _P, _P, _I64, _P, _I, _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),

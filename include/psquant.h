@@ -104,6 +104,15 @@ PSQ_API int psq_gemm_i8(const int8_t *a, int64_t lda, const float *a_scale, cons
 PSQ_API int psq_gemm_i8_i32(const int8_t *a, int64_t lda, const int8_t *w, int64_t ldw, int32_t *c,
                     int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
 
+/* psq_gemm_i8 with bf16 output, scheduled as 8 waves per workgroup (two per SIMD, 128 x 64 wave
+ * tiles) instead of 4: the same outputs bit for bit.  A comparison schedule with no counterpart in
+ * the reference, not used by the module path (it measures slower than psq_gemm_i8 on every shape
+ * tried); kept so that the comparison can be re-run.  N % 256 == 0, K % 256 == 0, y_dtype
+ * PSQ_BF16, 16-byte aligned a, w, y; ldy a multiple of 8. */
+PSQ_API int psq_gemm_i8_8wave(const int8_t *a, int64_t lda, const float *a_scale, const int8_t *w,
+                      int64_t ldw, const float *w_scale, const void *bias, int bias_dtype, void *y,
+                      int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void *stream);
+
 /* FP8 e4m3fn x e4m3fn -> fp32 accumulate on the gfx950 f8f6f4 MFMA, same epilogue.
  * w_scale is one fp32 (w_scale_per_row = 0) or [N] (1).  Replaces torch._scaled_mm for
  * float8_e4m3fn (powershard/quant_linear.py:32, 236-237). */

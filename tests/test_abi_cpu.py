@@ -42,6 +42,11 @@ def _fake(addr=0x10000):
     (lambda L: L.psq_gemm_i8(None, 128, _fake(), _fake(), 128, _fake(), None, 0, _fake(), 0, 16, 16, 16, 128, None), -1),
     # K not a multiple of 128
     (lambda L: L.psq_gemm_i8(_fake(), 96, _fake(), _fake(), 96, _fake(), None, 0, _fake(), 0, 16, 16, 16, 96, None), -2),
+    # the 8-wave comparison schedule: whole 256-column tiles and an even stage count only
+    (lambda L: L.psq_gemm_i8_8wave(_fake(), 256, _fake(), _fake(), 256, _fake(), None, 0, _fake(), 0, 128, 16, 128, 256,
+                                   None), -2),
+    (lambda L: L.psq_gemm_i8_8wave(_fake(), 384, _fake(), _fake(), 384, _fake(), None, 0, _fake(), 0, 256, 16, 256, 384,
+                                   None), -2),
     # misaligned operand
     (lambda L: L.psq_gemm_i8_i32(_fake(0x10008), 128, _fake(), 128, _fake(), 16, 16, 16, 128, None), -2),
     # bad output dtype

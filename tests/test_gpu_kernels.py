@@ -256,6 +256,36 @@ def test_gemm_i8_epilogue_subnormal(gpu, out_dtype):
     assert_bitexact(y, ref, "subnormal epilogue output")
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 512, 1024), (4100, 4096, 512), (8200, 2048, 768)])
+def test_gemm_i8_8wave_matches_gemm_i8(gpu, M, N, K):
+    """psq_gemm_i8_8wave, the 8-wave comparison schedule: bit-identical to psq_gemm_i8 (bf16 with
+    a bias) and to the oracle, partial row tiles and several tiles per workgroup included."""
+    import ctypes
+    from powershard_amd import _native
+    print(f"gemm_i8_8wave M={M} N={N} K={K}", flush=True)
+    g = seeded(M + 5 * N + K)
+    qa = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    sa = torch.rand(M, generator=g) * 0.05 + 1e-3
+    qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.rand(N, generator=g) * 1e-3 + 1e-5
+    b = (torch.randn(N, generator=g) * 0.5).to(torch.bfloat16)
+    lib = _native.lib()
+    st = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    args = [t.to(gpu) for t in (qa, sa, qw, sw, b)]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    ys = []
+    for fn in (lib.psq_gemm_i8, lib.psq_gemm_i8_8wave):
+        y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        rc = fn(P(args[0]), K, P(args[1]), P(args[2]), K, P(args[3]), P(args[4]), _native.BF16, P(y), _native.BF16,
+                N, M, N, K, st)
+        assert rc == 0, _native.last_error()
+        ys.append(y)
+    torch.cuda.synchronize()
+    assert_bitexact(ys[1], ys[0].cpu(), "8-wave against 4-wave output")
+    ref = oracle.epilogue_i32(oracle.gemm_i8_i32(qa, qw), sa, sw, b, out_dtype=torch.bfloat16)
+    assert_bitexact(ys[1], ref, "8-wave output against the oracle")
+
+
 # ---------------------------------------------------------------------------- fp8
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1000, 520, 5120), (17, 33, 128), (129, 777, 1024),
                                    (4100, 4000, 512), (4352, 4352, 256)])
