@@ -398,6 +398,14 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
         else
             acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
     };
+    // the same with a zero accumulator input (inline constant 0): a tile's first k-step, so the
+    // 256 accumulator registers need no clearing writes before the tile
+    auto mfma_first = [&](int i, int j, const FT (&fa)[TM], const FT (&fw)[TN]) {
+        if constexpr (FP8)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], Acc{}, WF, 0, 0, 127, 0, 127);
+        else
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], Acc{}, 0, 0, 0);
+    };
     // Reads in the order the MFMAs (row-major over i, j) first need them: A0, W0..W3, A1..A3.
     constexpr int kReadOrder[TM + TN] = {0, 4, 5, 6, 7, 1, 2, 3};
 
@@ -806,12 +814,13 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
     // k-step / stage of the steady state: stage kt + 2 still in the current tile, ring slot SL
     // known at compile time
     auto kstep_fast = [&](auto tc, auto slc, FT (&ca)[TM], FT (&cw)[TN], FT (&na)[TM], FT (&nw)[TN], int64_t k1,
-                          int64_t k2) {
+                          int64_t k2, auto firstc) {
         constexpr int t = decltype(tc)::value, SL = decltype(slc)::value;
         constexpr bool last = t == KS - 1;
         static_for<TM * TN>([&](auto pc) {
             constexpr int p = decltype(pc)::value;
-            mfma(p / TN, p % TN, ca, cw);
+            if constexpr (decltype(firstc)::value) mfma_first(p / TN, p % TN, ca, cw);
+            else mfma(p / TN, p % TN, ca, cw);
             if constexpr (p < TM + TN)
                 read_frag_c(std::integral_constant<int, last ? (SL ^ 1) : SL>{},
                             std::integral_constant<int, last ? 0 : t + 1>{},
@@ -824,22 +833,24 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
             __builtin_amdgcn_sched_barrier(0);
         });
     };
-    auto stage_fast = [&](auto slc, int kt) {
+    // firstc: the tile's first stage (its first k-step starts the accumulators from zero)
+    auto stage_fast = [&](auto slc, int kt, auto firstc) {
         const int64_t k1 = (int64_t)(kt + 1) * BK, k2 = (int64_t)(kt + 2) * BK;
         using I0 = std::integral_constant<int, 0>;
         using I1 = std::integral_constant<int, 1>;
+        using NO = std::false_type;
         if constexpr (!FP8) {
-            kstep_fast(I0{}, slc, fa0, fw0, fa1, fw1, k1, k2);
-            kstep_fast(I1{}, slc, fa1, fw1, fa0, fw0, k1, k2);
-            kstep_fast(std::integral_constant<int, 2>{}, slc, fa0, fw0, fa1, fw1, k1, k2);
+            kstep_fast(I0{}, slc, fa0, fw0, fa1, fw1, k1, k2, firstc);
+            kstep_fast(I1{}, slc, fa1, fw1, fa0, fw0, k1, k2, NO{});
+            kstep_fast(std::integral_constant<int, 2>{}, slc, fa0, fw0, fa1, fw1, k1, k2, NO{});
             wait_vmcnt<0>();
             stage_barrier();
-            kstep_fast(std::integral_constant<int, 3>{}, slc, fa1, fw1, fa0, fw0, k1, k2);
+            kstep_fast(std::integral_constant<int, 3>{}, slc, fa1, fw1, fa0, fw0, k1, k2, NO{});
         } else {
-            kstep_fast(I0{}, slc, fa0, fw0, fa1, fw1, k1, k2);
+            kstep_fast(I0{}, slc, fa0, fw0, fa1, fw1, k1, k2, firstc);
             wait_vmcnt<0>();
             stage_barrier();
-            kstep_fast(I1{}, slc, fa1, fw1, fa0, fw0, k1, k2);
+            kstep_fast(I1{}, slc, fa1, fw1, fa0, fw0, k1, k2, NO{});
         }
     };
     auto stage = [&](int kt) {
@@ -878,22 +889,43 @@ gemm_q8_kernel(const uint8_t *__restrict__ A, int64_t lda, const uint8_t *__rest
                 dow[j] = (int32_t)(qw[j] - ow[j]);
             }
         }
+        // an even stage count brings the ring back to slot 0 at every tile start: the steady state
+        // runs in pairs of stages with compile-time slots, the last two the general way.  int8:
+        // the first pair starts the accumulators from zero (c1 GEMM 1.789 -> 1.775 ms); fp8 clears
+        // them (its first-pair copy measured 0.9% slower at c3)
+        auto clear_acc = [&] {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+            for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++)
+                for (int j = 0; j < TN; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        };
         int kt0 = 0;
-        if ((nk & 1) == 0) {
-            set_lof();
-            set_rsrc();
-            // an even stage count brings the ring back to slot 0 at every tile start: the steady
-            // state runs in pairs of stages with compile-time slots, the last two the general way
+        if constexpr (!FP8) {
+            if ((nk & 1) == 0 && nk >= 4) {
+                set_lof();
+                set_rsrc();
+                stage_fast(std::integral_constant<int, 0>{}, 0, std::true_type{});
+                stage_fast(std::integral_constant<int, 1>{}, 1, std::false_type{});
 #pragma clang loop unroll(disable)
-            for (; kt0 + 3 < nk; kt0 += 2) {
-                stage_fast(std::integral_constant<int, 0>{}, kt0);
-                stage_fast(std::integral_constant<int, 1>{}, kt0 + 1);
+                for (kt0 = 2; kt0 + 3 < nk; kt0 += 2) {
+                    stage_fast(std::integral_constant<int, 0>{}, kt0, std::false_type{});
+                    stage_fast(std::integral_constant<int, 1>{}, kt0 + 1, std::false_type{});
+                }
+            } else {
+                clear_acc();
+            }
+        } else {
+            clear_acc();
+            if ((nk & 1) == 0) {
+                set_lof();
+                set_rsrc();
+#pragma clang loop unroll(disable)
+                for (; kt0 + 3 < nk; kt0 += 2) {
+                    stage_fast(std::integral_constant<int, 0>{}, kt0, std::false_type{});
+                    stage_fast(std::integral_constant<int, 1>{}, kt0 + 1, std::false_type{});
+                }
             }
         }
 #pragma clang loop unroll(disable)
