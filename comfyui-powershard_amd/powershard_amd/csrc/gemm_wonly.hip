@@ -1626,16 +1626,24 @@ TiledPlan plan_tiled(int64_t M, int64_t N, int64_t K, int cus, bool allow_sk)
 // The weight-streaming kernel takes the uint4 shapes with M <= SKINNY_MAX_M and groups of a
 // multiple of 128; the skinny kernel takes M <= SKINNY_MAX_M when K is a whole number of
 // 128-element blocks (and, for uint4, the groups hold whole 32-element lane runs); the tiled
-// kernel takes the rest.
+// kernel takes the rest.  One exception with a split-K workspace (`ws`): a streaming grid of at
+// most half the CUs (N up to 64 x 128 columns on 256 CUs) over a long K (>= 8192) goes to the tiled
+// kernel's stream-K, which spreads the K range over every CU (64 x 5120 x 13824: 103.8 -> 51.9 us;
+// 64 x 5120 x 25600: 150.9 -> 62.5 us).  At K = 5120 the streaming kernel stays ahead (33.8 against
+// 37.0 us at 64 x 5120), and without a workspace the tiled kernel could not split.
 enum class Path { Decode, Stream, Skinny, Tiled };
 
-Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
+Path choose_path(int wk, int64_t ldx, int64_t M, int64_t N, int64_t K, int gs, bool ws, int cus)
 {
     if (wk == W_UINT4 && M <= wd::MAXM && gs % 128 == 0 && K % 512 == 0 && decode_depth(M, K, false) > 0 &&
         ldx <= (1LL << 22))
         return Path::Decode;
-    if (wk == W_UINT4 && M <= SKINNY_MAX_M && gs % 128 == 0 && K % ws::STEP == 0 && ldx <= (1LL << 22))
+    if (wk == W_UINT4 && M <= SKINNY_MAX_M && gs % 128 == 0 && K % ws::STEP == 0 && ldx <= (1LL << 22)) {
+        if (ws && cus > 0 && 2 * ((N + ws::ROWS - 1) / ws::ROWS) <= cus && K >= 8192 && K <= (1LL << 22) &&
+            plan_tiled(M, N, K, cus, true).sk > 0)
+            return Path::Tiled;
         return Path::Stream;
+    }
     if (M <= SKINNY_MAX_M && K % SK_BLOCK == 0 && (wk != W_UINT4 || gs % 32 == 0)) return Path::Skinny;
     return Path::Tiled;
 }
@@ -1644,11 +1652,12 @@ Path choose_path(int wk, int64_t ldx, int64_t M, int64_t K, int gs)
 int64_t workspace_bytes(int wk, int64_t ldx, int64_t M, int64_t N, int64_t K, int gs)
 {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const Path path = choose_path(wk, ldx, M, K, gs);
-    if (path != Path::Tiled) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    return plan_tiled(M, N, K, cu_count(dev), true).ws_bytes;
+    const int cus = cu_count(dev);
+    const Path path = choose_path(wk, ldx, M, N, K, gs, true, cus);
+    if (path != Path::Tiled) return 0;
+    return plan_tiled(M, N, K, cus, true).ws_bytes;
 }
 
 // workspace: NULL = data-parallel tiles only; else at least workspace_bytes(), its counter words
@@ -1659,10 +1668,10 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
            void *workspace, int64_t ws_bytes, hipStream_t st, const char *name)
 {
     const uint16_t *xp = (const uint16_t *)x;
-    Path path = choose_path(WK, ldx, M, K, wa.gs);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
+    Path path = choose_path(WK, ldx, M, N, K, wa.gs, workspace != nullptr, cu_count(dev));
     if (path == Path::Decode) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
         const DecodePlan plan = plan_decode(M, N, K, wa.gs, wa.scale16, wa.zero16, cu_count(dev));
         if (plan.G > 0)
             return x_dtype == PSQ_BF16 ? launch_decode<PSQ_BF16>(xp, ldx, M, N, K, wa, plan, st, name)
@@ -1679,8 +1688,6 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
     }
     if (ldx > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: ldx above 2^22", name);   // 32-bit row offsets
     if (K > (1LL << 22)) return set_error(PSQ_E_SHAPE, "%s: K above 2^22", name);       // (of the weights too)
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
     const TiledPlan plan = plan_tiled(M, N, K, cu_count(dev), workspace != nullptr);
     wa.sk = 0;
     if (plan.sk) {

@@ -312,7 +312,9 @@ def test_gemm_fp8(gpu, M, N, K, per_row):
 # M <= 64 runs a weight-streaming kernel (groups of a multiple of 128 and K of 256: the streaming
 # one -- its scale / zero tables whole in LDS when K / g is a multiple of 8 up to 40 and M <= 48, in
 # blocks of 8 groups for other multiples of 8, per step otherwise; else, with K % 128 == 0, the
-# split-K one), the rest the tiled one
+# split-K one), the rest the tiled one.  With the package's workspace, a streaming grid of at most
+# half the CUs over K >= 8192 runs the tiled kernel's stream-K instead (12 x 600 x 12288,
+# 50 x 256 x 8192, 16 x 5120 x 13824, 64 x 1024 x 25600)
 @pytest.mark.parametrize("M,N,K,gs", [(512, 384, 1024, 128), (7, 256, 512, 64), (130, 100, 5120, 128),
                                       (64, 1000, 256, 256), (1, 2600, 5120, 128), (16, 513, 1024, 128),
                                       (33, 64, 2048, 64), (65, 300, 1024, 128), (3, 100, 384, 64),
@@ -321,7 +323,8 @@ def test_gemm_fp8(gpu, M, N, K, per_row):
                                       (64, 129, 640, 128), (17, 1100, 5120, 128), (48, 256, 1536, 384),
                                       (9, 200, 768, 384), (5, 200, 640, 128), (16, 1024, 5120, 128),
                                       (40, 700, 4096, 128), (24, 1300, 2048, 256), (56, 384, 5120, 128),
-                                      (12, 600, 12288, 128), (50, 256, 8192, 256), (60, 200, 3072, 256)])
+                                      (12, 600, 12288, 128), (50, 256, 8192, 256), (60, 200, 3072, 256),
+                                      (16, 5120, 13824, 128), (64, 1024, 25600, 128)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
     from powershard_amd import ops
