@@ -476,10 +476,11 @@ class _Installer:
     swaps in the QuantLinear modules and builds the report."""
 
     def __init__(self, tensors, weight_format, compute, scope, compute_dtype, device, name_map, follow_input,
-                 quant_options):
+                 quant_options, open_file=None):
         self.tensors, self.weight_format, self.compute = tensors, weight_format, compute
         self.scope, self.compute_dtype, self.device = scope, compute_dtype, device
         self.name_map, self.follow_input, self.options = name_map, follow_input, quant_options or {}
+        self.open_file = open_file
         self.templates, self.natives = {}, {}
         self.report = dict(weight_format=weight_format, compute=compute, modules={}, skipped=0, stored_bytes=0)
 
@@ -514,8 +515,19 @@ class _Installer:
         signature = ("file", fmt, json_key(desc["comfy_quant"]), tuple(shape),
                      tuple((n[len(module):], str(dt), tuple(sh)) for n, (dt, sh) in sorted(own.items())))
         if signature not in self.templates:
-            self.templates[signature] = quantized_from_file(None, own, module, desc["comfy_quant"], shape,
-                                                            self.device, self.compute_dtype, meta=True)
+            # powershard/quant_linear.py:329-337: a template that cannot be built from shapes alone is
+            # built from the module's real tensors, read on the CPU through open_file(table, key)
+            try:
+                qt = quantized_from_file(None, own, module, desc["comfy_quant"], shape, self.device,
+                                         self.compute_dtype, meta=True)
+            except Exception:
+                if self.open_file is None:
+                    raise
+                handle = self.open_file(table, key)
+                real = {n: d["key"] for n, d in _module_tensors(table, module).items()}
+                qt = quantized_from_file(handle, real, module, desc["comfy_quant"], shape, torch.device("cpu"),
+                                         self.compute_dtype)
+            self.templates[signature] = qt
         source = dict(kind="file", table=table, module=module, conf=desc["comfy_quant"], key=key)
         return self.templates[signature], source, extras
 
@@ -569,13 +581,15 @@ def install_quant_linears(net, tensors, weight_format, compute, scope, compute_d
     name_map: parameter name -> (table, name in table) for multi-file models.
     quant_options (this package's addition): layout options of quantize-at-load weights, e.g.
     {"convrot": True, "convrot_groupsize": 256} for int8 or {"group_size": 128} for int4.
-    open_file is accepted for the reference's signature; every template here is built from shapes.
+    open_file(table, key) -> a handle with get_tensor(name): used, as in the reference, only when a
+    file module's template cannot be built from its shapes; the template then comes from the
+    module's real tensors on the CPU.
     Returns a report.
     """
     if weight_format in UNSUPPORTED_TARGETS:
         raise ValueError(f"weight_format {weight_format} is a Blackwell block format, not supported on MI355X")
     installer = _Installer(tensors, weight_format, compute, scope, compute_dtype, device, name_map, follow_input,
-                           quant_options)
+                           quant_options, open_file)
     if weight_format != "dequantize":
         for name, module in list(net.named_modules()):
             if installer.eligible(name, module):

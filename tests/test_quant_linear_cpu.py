@@ -280,6 +280,50 @@ def test_convrot_file_module_loads_as_file_and_matches_dequantize_rows(tmp_path)
     torch.testing.assert_close(layer(x).float(), ref.float(), atol=2e-2, rtol=2e-2)
 
 
+def test_open_file_builds_the_template_when_shapes_are_not_enough(tmp_path, monkeypatch):
+    """powershard/quant_linear.py:329-337: when a file template cannot be built from shapes (meta
+    tensors), install_quant_linears opens the file through open_file(table, key) and builds it from
+    the real tensors; without open_file the error propagates.  Forced here by a decoder that refuses
+    meta tensors, as a format whose layout depends on the data would."""
+    from safetensors import safe_open
+    conf = json.load(open(os.path.join(GOLDEN, "convrot_config.json")))
+    w = torch.randn(32, 512)
+    q, s = oracle.quantize_weight_int8(w, True, 256)
+    path = _save(tmp_path, {"m.weight": q, "m.weight_scale": s, "m.bias": torch.zeros(32)}, conf)
+    table, _ = _table(path)
+    real_from_file = ql.quantized_from_file
+
+    def needs_data(handle, entries, module, conf, shape, device, dtype, meta=False):
+        if meta:
+            raise RuntimeError("this layout needs the data")
+        return real_from_file(handle, entries, module, conf, shape, device, dtype, meta)
+    monkeypatch.setattr(ql, "quantized_from_file", needs_data)
+    with pytest.raises(RuntimeError, match="needs the data"):
+        ql.install_quant_linears(nn.ModuleDict({"m": nn.Linear(512, 32).to(torch.bfloat16)}), table, "as_file",
+                                 "dequantize", None, torch.bfloat16, "cpu")
+    opened = []
+    with safe_open(str(path), framework="pt") as f:
+        def open_file(tab, key):
+            opened.append(key)
+            return f
+        net = nn.ModuleDict({"m": nn.Linear(512, 32).to(torch.bfloat16), "n": nn.Linear(512, 32).to(torch.bfloat16)})
+        table2 = dict(table)
+        for k in [k for k in table if k.startswith("m.")]:   # a second module of the same layout
+            table2["n." + k[2:]] = dict(table[k], key=k)
+        report = ql.install_quant_linears(net, table2, "as_file", "dequantize", None, torch.bfloat16, "cpu",
+                                          open_file=open_file)
+        assert opened == ["m.weight"], "one template per layout signature, opened once"
+        assert report["modules"]["int8_tensorwise"]["count"] == 2
+        monkeypatch.setattr(ql, "quantized_from_file", real_from_file)
+        layer = net["m"]
+        full, _ = ql.build_bytes(layer, f, "cpu")
+    layer.qbytes = nn.Parameter(full, requires_grad=False)
+    layer.bias = None
+    x = torch.randn(5, 512, dtype=torch.bfloat16)
+    ref = torch.nn.functional.linear(x, dequantize_rows(q, s, True, 256, torch.bfloat16))
+    torch.testing.assert_close(layer(x).float(), ref.float(), atol=2e-2, rtol=2e-2)
+
+
 def test_quantize_at_load_from_bf16_file(tmp_path):
     from safetensors import safe_open
     w = torch.randn(64, 256, dtype=torch.bfloat16)
