@@ -340,6 +340,37 @@ def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
     assert_fp32_path(y32, yb, ref32, "w4a16 gemm")
 
 
+@pytest.mark.parametrize("M,N,K", [(32, 1024, 16384), (64, 640, 8192)])
+def test_gemm_w4a16_long_k_small_n_both_routes(gpu, M, N, K):
+    """A streaming grid of few workgroups over a long K: with the split-K workspace the tiled
+    kernel's stream-K takes it, without one (psq_gemm_w4a16) the weight-streaming kernel.  Both
+    meet the bar against the oracle and agree with each other within it."""
+    import ctypes
+    from powershard_amd import _native, ops
+    print(f"w4a16 long-K small-N M={M} N={N} K={K}", flush=True)
+    gs = 128
+    lib = _native.lib()
+    assert lib.psq_gemm_wonly_workspace_bytes(_native.W_UINT4, K, M, N, K, gs) > 0, "the shape must split K"
+    x = heavy_rows(M, K, seed=M + K, outlier_frac=0)
+    w = torch.randn(N, K, generator=seeded(N + 1)) * 0.02
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    b = (torch.randn(N, generator=seeded(9)) * 0.01).to(torch.bfloat16)
+    xg, wqg, sg, zg, bg = (t.to(gpu) for t in (x, wq, s, z, b))
+    y_split = ops.gemm_w4a16(xg, wqg, sg, zg, gs, bg, out_dtype=torch.float32)
+    y_stream = torch.full((M, N), float("nan"), dtype=torch.float32, device=gpu)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    rc = lib.psq_gemm_w4a16(P(xg), _native.BF16, K, P(wqg), P(sg), P(zg), gs, P(bg), _native.BF16, P(y_stream),
+                            _native.F32, N, M, N, K, st)
+    assert rc == 0, _native.last_error()
+    torch.cuda.synchronize()
+    ref = oracle.gemm_wonly(x, oracle.dequant_uint4(wq, s, z, gs), None, b, out_dtype=torch.float32)
+    rms = ref.pow(2).mean().sqrt().item()
+    for name, y in (("stream-K", y_split), ("streaming", y_stream)):
+        assert (y.cpu() - ref).abs().max().item() <= 1e-2 * rms, name
+    assert (y_split - y_stream).abs().max().item() <= 1e-2 * rms
+
+
 @pytest.mark.parametrize("M,N,K", [(1024, 512, 1024), (5, 40, 256), (200, 300, 5120), (1, 1030, 5120),
                                    (48, 256, 1024), (64, 64, 640), (700, 512, 640), (257, 1024, 192)])
 def test_gemm_w8a16(gpu, M, N, K):
