@@ -1120,9 +1120,11 @@ constexpr int MAXM = 8;
 constexpr int TROWS = 128;                            // rows of the scale / zero table
 constexpr int SZT_MAX = 2 * TROWS * 40 * 2;           // 20 KB: G <= 40
 __host__ __device__ inline int64_t xrow(int64_t K) { return 2 * K + 16; } // padded activation row in LDS (bytes)
+constexpr int MAXU = 32;                              // units per workgroup
+constexpr int BIASB = MAXU * 16 * 4;                  // the workgroup's bias values, one word each
 inline int64_t lds_bytes(int64_t M, int64_t K, int D, bool szt)
 {
-    return M * xrow(K) + (int64_t)NW * D * (WBYTES + (szt ? 0 : SZW)) + (szt ? SZT_MAX : 0);
+    return M * xrow(K) + (int64_t)NW * D * (WBYTES + (szt ? 0 : SZW)) + (szt ? SZT_MAX : 0) + BIASB;
 }
 // The wave's 16 weight rows are 128 bytes each, lane (n, h) reading chunks 2 h and 2 h + 1 of row n:
 // chunk c of row r sits at c ^ dsw(r), row bits (3, 1, 2) -> chunk bits (0, 1, 2), a placement free of
@@ -1157,9 +1159,20 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     auto wowner = [&](int t) { return ((t + 1) * NW + I - 1) / I - 1; };  // the wave holding relative item t
     const int64_t t0 = ua * nb + wrun(wave), t1 = ua * nb + wrun(wave + 1);
     uint8_t *const tab = smem + (int64_t)M * xr;                                  // [scale | zero][row][G]
-    uint8_t *const ring0 = tab + (SZT ? SZT_MAX : 0);
+    uint8_t *const bl = tab + (SZT ? SZT_MAX : 0);                                // bias, word per column
+    uint8_t *const ring0 = bl + BIASB;
     uint8_t *const ring = ring0 + (int64_t)wave * D * WS;
     const int64_t trow0 = 16 * ua;                     // the table's first row
+
+    // the bias of the workgroup's columns, column i of the range in word i (global->LDS: a register
+    // load at a unit's end made the compiler drain the wave's ring before the store)
+    if (wa.bias && 64 * wave < 16 * (ub - ua)) {
+        const int64_t n = min(16 * ua + 64 * wave + lane, (int64_t)N - 1);
+        if (wa.bias_dtype == PSQ_F32)
+            __builtin_amdgcn_global_load_lds((glb_ptr)((const float *)wa.bias + n), (lds_ptr)(bl + 256 * wave), 4, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds((glb_ptr)((const uint16_t *)wa.bias + n), (lds_ptr)(bl + 256 * wave), 2, 0, 0);
+    }
 
     // the activations: row m at m * xr, 1 KB per wave load (K % 512 == 0: whole loads per row)
     const int per_row = (int)(2 * (int64_t)K / 1024), nx = M * per_row;
@@ -1312,7 +1325,12 @@ gemm_w4_decode(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K,
     auto store = [&](int64_t c, v4f v) {
         const int64_t n = 16 * c + nr;
         if (n >= N) return;
-        const float bb = wa.bias ? load_elem(wa.bias, n, wa.bias_dtype) : 0.0f;
+        float bb = 0.0f;
+        if (wa.bias) {
+            const uint32_t bw = ((const uint32_t *)bl)[16 * (c - ua) + nr];
+            bb = wa.bias_dtype == PSQ_F32 ? __uint_as_float(bw) : wa.bias_dtype == PSQ_BF16 ? bf16_to_f32(bw & 0xffffu)
+                                                                                             : f16_to_f32(bw);
+        }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int m = 4 * h + r;
@@ -1435,6 +1453,7 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int gs, const void *scal
     p.G = std::min<int64_t>(units, cus);
     const int64_t upw = (units + p.G - 1) / p.G;                 // units per workgroup, at most
     if (upw * (K / wd::B) * wd::NW >= (1LL << 31)) p.G = 0;      // a workgroup's runs need 32-bit item numbers
+    if (upw > wd::MAXU) p.G = 0;                                  // its bias words in LDS
     p.szt = G % 8 == 0 && G <= 40 && upw <= wd::TROWS / 16 && ((uintptr_t)scale & 15) == 0 &&
             ((uintptr_t)zero & 15) == 0;
     p.depth = decode_depth(M, K, p.szt);
@@ -1473,6 +1492,223 @@ int launch_decode(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t 
         }
     };
     return p.szt ? go(std::true_type{}) : go(std::false_type{});
+}
+
+// ------------------------------------------------------ uint4 decode kernel, K split over the waves
+// One or two tokens (M <= 2) with 1024 <= K <= 6144.  One workgroup per CU takes a contiguous range
+// of 16-column units (as the kernel above); its 8 waves split K instead of the items: wave w owns
+// the 128-k half blocks [w H / 8, (w + 1) H / 8) of every unit (H = K / 128, at most XMAX), so it
+// loads its activation fragments into registers once, from global memory, and its loop reads only
+// weights (and scales) from LDS.  Each wave streams its (unit, half block) items, unit after unit,
+// through a private ring of D 1 KB slots (16 rows x 64 bytes: one global->LDS load each), all D in
+// flight from the start.  At the end of a unit the waves' partial sums meet in LDS behind one
+// barrier, and one wave adds them in wave order and stores the unit.  The arithmetic per weight is
+// the kernel above's (w = round_16(fmaf(q, s, -z s)), 16x16x32 MFMA, activations as the A operand).
+// Measured at N = 25600, K = 5120 on one host, alternating launches: M = 1 21.4 us against 23.8 us
+// of the kernel above, M = 2 21.9 / 22.7 us; at M = 4 it was even and at M = 8 slower (24.1 /
+// 22.3 us), so those stay with the kernel above.  Ring depths 4 / 6 / 8 gave 21.4 / 22.0 / 22.1 us.
+namespace wx {
+constexpr int NW = 8;                          // waves per workgroup
+constexpr int HB = 128;                        // k per item (half block)
+constexpr int XMAX = 6;                        // half blocks per wave: K <= NW * XMAX * HB = 6144
+constexpr int MAXM = 2;                        // rows
+constexpr int WB = 16 * HB / 2;                // an item's nibbles (1 KB)
+constexpr int SZW = 256;                       // an item's scale / zero words (no table)
+constexpr int RED = 2 * NW * 1024;             // two sets of the waves' partial sums
+constexpr int BIASB = wd::BIASB;               // the workgroup's bias values (at most wd::MAXU units)
+constexpr int D = 4;                           // ring depth
+inline int lds_bytes(bool szt) { return (szt ? wd::SZT_MAX : 0) + RED + BIASB + NW * D * (WB + (szt ? 0 : SZW)); }
+// chunk c (16 bytes) of row r of an item sits at position c ^ psw(r): the 16 lanes (r, c) of one
+// ds_read_b128 lane group then cover the 64 banks once
+__device__ __forceinline__ int psw(int r) { return (r >> 2) & 3; }
+}  // namespace wx
+
+template <int XDT, bool SZT>
+__global__ void __launch_bounds__(wx::NW * 64)
+gemm_w4_decode_ks(const uint16_t *__restrict__ x, int64_t ldx, int M, int N, int K, WArgs wa)
+{
+    using namespace wx;
+    using XV = typename std::conditional<XDT == PSQ_BF16, v8bf, v8h>::type;
+    constexpr int WS = WB + (SZT ? 0 : SZW);
+    constexpr int LOADS = SZT ? 1 : 2;                 // ring loads per item
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nr = lane & 15, h = lane >> 4;
+    const int G = K / wa.gs, hg = wa.gs / HB, H = K / HB;
+    const int64_t wld = K / 2;
+    const int64_t units = (N + 15) / 16;
+    const int64_t ua = wd::run_start(blockIdx.x, units, gridDim.x), ub = wd::run_start(blockIdx.x + 1, units, gridDim.x);
+    const int h0 = wave * H / NW, cnt = (wave + 1) * H / NW - h0;    // K >= 1024: cnt >= 1
+    const int I = (int)(ub - ua) * cnt;                              // this wave's items
+    uint8_t *const tab = smem;                                       // [scale | zero][row][G] (SZT)
+    float *const red = (float *)(smem + (SZT ? wd::SZT_MAX : 0));
+    uint8_t *const bl = smem + (SZT ? wd::SZT_MAX : 0) + RED;
+    uint8_t *const ring = bl + BIASB + wave * D * WS;
+    const int64_t trow0 = 16 * ua;
+
+    // the bias of the workgroup's columns, column i of the range in word i (global->LDS: a register
+    // load would make the compiler drain the ring before the first store that uses it)
+    if (wa.bias && 64 * wave < 16 * (ub - ua)) {
+        const int64_t n = min(16 * ua + 64 * wave + lane, (int64_t)N - 1);
+        if (wa.bias_dtype == PSQ_F32)
+            __builtin_amdgcn_global_load_lds((glb_ptr)((const float *)wa.bias + n), (lds_ptr)(bl + 256 * wave), 4, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds((glb_ptr)((const uint16_t *)wa.bias + n), (lds_ptr)(bl + 256 * wave), 2, 0, 0);
+    }
+    // the scale and zero rows of the workgroup's units (as the kernel above)
+    if constexpr (SZT) {
+        const int tb = wd::TROWS * G * 2, nl = (tb + 1023) / 1024;
+        const int64_t valid = min((int64_t)wd::TROWS, (int64_t)N - trow0) * G * 2;
+        for (int i = wave; i < 2 * nl; i += NW) {
+            const int arr = i >= nl, j = i - arr * nl, off = j * 1024 + 16 * lane;
+            const uint8_t *src = (const uint8_t *)((arr ? wa.zero16 : wa.scale16) + trow0 * G);
+            if (off < tb)
+                __builtin_amdgcn_global_load_lds((glb_ptr)(src + min((int64_t)off, valid - 16)),
+                                                 (lds_ptr)(tab + arr * tb + j * 1024), 16, 0, 0);
+        }
+    }
+    // the activation fragments: lane (n, h) of k-step t of half block j carries k = 128 (h0 + j) +
+    // 32 h + 8 t .. + 7 of row min(n, M - 1); entries past the wave's last half block repeat it
+    // (loaded, never used).  Loaded before the ring, so the wait below covers them.
+    XV xf[XMAX][4];
+    {
+        const uint16_t *xr = x + (int64_t)min(nr, M - 1) * ldx + 32 * h;
+#pragma unroll
+        for (int j = 0; j < XMAX; j++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                xf[j][t] = __builtin_bit_cast(XV, *(const v4i *)(xr + (h0 + min(j, cnt - 1)) * HB + 8 * t));
+    }
+    // the ring: item ti = (unit iu, half block h0 + ij); past the last item the last again (into a
+    // slot nobody reads).  The unit's row addresses (rows past N clamped) are set when it changes.
+    int ti = 0, ij = 0;
+    int64_t iu = ua;
+    const int lr = lane >> 2, lc = (lane & 3) ^ psw(lane >> 2);
+    const uint8_t *wrow = nullptr;
+    const uint16_t *srow = nullptr;
+    auto set_unit = [&] {
+        wrow = wa.wq + min(16 * iu + lr, (int64_t)N - 1) * wld + h0 * (HB / 2) + 16 * lc;
+        if constexpr (!SZT) srow = (h & 1 ? wa.zero16 : wa.scale16) + min(16 * iu + nr, (int64_t)N - 1) * G;
+    };
+    set_unit();
+    auto issue = [&](int slot) {
+        uint8_t *const sl = ring + slot * WS;
+        __builtin_amdgcn_global_load_lds((glb_ptr)(wrow + ij * (HB / 2)), (lds_ptr)sl, 16, 0, 0);
+        if constexpr (!SZT)     // lane 16 a + n: array a & 1 (scale, zero) of row n, into word lane
+            __builtin_amdgcn_global_load_lds((glb_ptr)(srow + (h0 + ij) / hg), (lds_ptr)(sl + WB), 2, 0, 0);
+        if (ti + 1 < I) {
+            ti++;
+            if (++ij == cnt) {
+                ij = 0;
+                iu++;
+                set_unit();
+            }
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);       // the ring loads after the activation loads (the wait counts on it)
+    for (int s = 0; s < D; s++) issue(s);
+    wait_vmcnt<LOADS * D>();                 // this wave's bias, table and activation loads landed
+    stage_barrier();                         // ... and every other wave's
+
+    auto store = [&](int64_t c, v4f v) {
+        const int64_t n = 16 * c + nr;
+        if (n >= N) return;
+        float bb = 0.0f;
+        if (wa.bias) {
+            const uint32_t bw = ((const uint32_t *)bl)[16 * (c - ua) + nr];
+            bb = wa.bias_dtype == PSQ_F32 ? __uint_as_float(bw) : wa.bias_dtype == PSQ_BF16 ? bf16_to_f32(bw & 0xffffu)
+                                                                                             : f16_to_f32(bw);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 4 * h + r;
+            if (m < M) store_elem(wa.y, (int64_t)m * wa.ldy + n, wa.y_dtype, v[r] + bb);
+        }
+    };
+    const int wpos = 16 * (h ^ psw(nr));
+    int slot = 0;
+    for (int64_t u = ua; u < ub; u++) {
+        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < XMAX; j++) {
+            if (j < cnt) {
+                wait_vmcnt<LOADS * (D - 1)>();   // this item's loads landed
+                const uint8_t *const sl = ring + slot * WS;
+                const v4i wv = *(const v4i *)(sl + nr * 64 + wpos);
+                float sv, zv;
+                if constexpr (SZT) {
+                    const uint16_t *tb16 = (const uint16_t *)tab;
+                    const int row = (int)(16 * (u - ua)) + nr, g = (h0 + j) / hg;
+                    sv = f16_to_f32(tb16[row * G + g]);
+                    zv = f16_to_f32(tb16[(wd::TROWS + row) * G + g]);
+                } else {
+                    const uint32_t *sz = (const uint32_t *)(sl + WB);
+                    sv = f16_to_f32(sz[nr]);
+                    zv = f16_to_f32(sz[16 + nr]);
+                }
+                const float zs = -(zv * sv), s24 = sv * kTwo24, s20 = sv * kTwo20;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const Nib4 v = nib_split((uint32_t)wv[t]);
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) w[e] = dq_pair_u4<XDT>(v, e, s24, s20, zs);
+                    const XV wf = __builtin_bit_cast(XV, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+                    if constexpr (XDT == PSQ_BF16) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[j][t], wf, acc, 0, 0, 0);
+                    else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j][t], wf, acc, 0, 0, 0);
+                }
+                // the slot's data are used; the refill may not move above that (lifted above the
+                // compute, the load into LDS overtook the read of the same slot)
+                __builtin_amdgcn_sched_barrier(0);
+                issue(slot);
+                slot = slot == D - 1 ? 0 : slot + 1;
+            }
+        }
+        // the unit's partial sums, set (u - ua) % 2, wave after wave; one wave adds them in wave order
+        float *const rb = red + ((u - ua) & 1) * NW * 256;
+        *(v4f *)(rb + (wave * 64 + lane) * 4) = acc;
+        stage_barrier();
+        if (wave == (int)((u - ua) % NW)) {
+            v4f s = *(const v4f *)(rb + lane * 4);
+#pragma unroll
+            for (int w = 1; w < NW; w++) s = s + *(const v4f *)(rb + (w * 64 + lane) * 4);
+            store(u, s);
+        }
+    }
+    wait_vmcnt<0>();                         // the re-issued tail loads, before the workgroup ends
+}
+
+// Whether the K-split decode kernel takes a decode shape (planned as for the kernel above): at most
+// MAXM rows and half blocks that split over the waves within XMAX each.
+bool decode_ks_fits(int64_t M, int64_t K, const DecodePlan &p)
+{
+    return p.G > 0 && M <= wx::MAXM && K % wx::HB == 0 && K >= wx::HB * wx::NW && K <= wx::HB * wx::NW * wx::XMAX;
+}
+
+template <int XDT, bool SZT>
+int launch_decode_ks_s(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa, int64_t G,
+                       hipStream_t st, const char *name)
+{
+    auto kern = gemm_w4_decode_ks<XDT, SZT>;
+    const int lds = wx::lds_bytes(SZT);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(PSQ_E_DEVICE, "%s: no device", name);
+    static bool attr_set[64] = {};
+    if (dev < 64 && !attr_set[dev]) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+            return set_error(PSQ_E_DEVICE, "%s: cannot reserve %d bytes of LDS", name, lds);
+        attr_set[dev] = true;
+    }
+    kern<<<dim3((unsigned)G), dim3(wx::NW * 64), lds, st>>>(x, ldx, (int)M, (int)N, (int)K, wa);
+    return check_launch(name);
+}
+
+template <int XDT>
+int launch_decode_ks(const uint16_t *x, int64_t ldx, int64_t M, int64_t N, int64_t K, const WArgs &wa,
+                     const DecodePlan &p, hipStream_t st, const char *name)
+{
+    return p.szt ? launch_decode_ks_s<XDT, true>(x, ldx, M, N, K, wa, p.G, st, name)
+                 : launch_decode_ks_s<XDT, false>(x, ldx, M, N, K, wa, p.G, st, name);
 }
 
 template <int XDT, int MT, int SZM>
@@ -1673,6 +1909,9 @@ int launch(const void *x, int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_
     Path path = choose_path(WK, ldx, M, N, K, wa.gs, workspace != nullptr, cu_count(dev));
     if (path == Path::Decode) {
         const DecodePlan plan = plan_decode(M, N, K, wa.gs, wa.scale16, wa.zero16, cu_count(dev));
+        if (decode_ks_fits(M, K, plan))
+            return x_dtype == PSQ_BF16 ? launch_decode_ks<PSQ_BF16>(xp, ldx, M, N, K, wa, plan, st, name)
+                                       : launch_decode_ks<PSQ_F16>(xp, ldx, M, N, K, wa, plan, st, name);
         if (plan.G > 0)
             return x_dtype == PSQ_BF16 ? launch_decode<PSQ_BF16>(xp, ldx, M, N, K, wa, plan, st, name)
                                        : launch_decode<PSQ_F16>(xp, ldx, M, N, K, wa, plan, st, name);

@@ -309,6 +309,10 @@ def test_gemm_fp8(gpu, M, N, K, per_row):
 
 
 # ------------------------------------------------------------------- weight-only
+# M <= 8 with groups of a multiple of 128 runs a decode kernel: the K-split one for M <= 2 and
+# 1024 <= K <= 6144 (1 x 2600 x 5120, 2 x 300 x 1280 with per-item scales, 2 x 20000 x 4608 with
+# several units per workgroup, 1 x 25600 x 5120), the item-split one otherwise (5 x 200 x 640,
+# 4 x 300 x 7168, 8 x 4000 x 6144, 3 x 1000 x 4608).
 # M <= 64 runs a weight-streaming kernel (groups of a multiple of 128 and K of 256: the streaming
 # one -- its scale / zero tables whole in LDS when K / g is a multiple of 8 up to 40 and M <= 48, in
 # blocks of 8 groups for other multiples of 8, per step otherwise; else, with K % 128 == 0, the
@@ -324,7 +328,9 @@ def test_gemm_fp8(gpu, M, N, K, per_row):
                                       (9, 200, 768, 384), (5, 200, 640, 128), (16, 1024, 5120, 128),
                                       (40, 700, 4096, 128), (24, 1300, 2048, 256), (56, 384, 5120, 128),
                                       (12, 600, 12288, 128), (50, 256, 8192, 256), (60, 200, 3072, 256),
-                                      (16, 5120, 13824, 128), (64, 1024, 25600, 128)])
+                                      (16, 5120, 13824, 128), (64, 1024, 25600, 128), (4, 300, 7168, 128),
+                                      (8, 4000, 6144, 128), (3, 1000, 4608, 256), (2, 20000, 4608, 128),
+                                      (1, 25600, 5120, 128)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemm_w4a16(gpu, M, N, K, gs, xdt):
     from powershard_amd import ops

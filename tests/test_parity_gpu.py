@@ -345,24 +345,56 @@ def _fma_form_weights(wq, s, z, gs, cols, dtype):
     return (q * sg.double() + c.double()).float().to(dtype).float()
 
 
-@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M", [4, 48, 160])      # decode, streaming, tiled (split-K) kernels
-def test_w4a16_dequantized_weights_exact(gpu, M, xdt):
-    """One-hot activation rows make every output one dequantized weight (the MFMA adds zeros to a
-    single product), so each kernel's uint4 dequantization -- the nibble as an fp16 subnormal into
-    v_fma_mix_f32 -- is checked bit for bit against round_16(fmaf(q, s, -z s))."""
-    from powershard_amd import ops
-    K, N, gs = 1024, 640, 128
-    w = torch.randn(N, K, generator=seeded(110)) * 0.02
+def _one_hot_case(M, K, xdt, seed=110):
+    N, gs = 640, 128
+    w = torch.randn(N, K, generator=seeded(seed)) * 0.02
     w[:, :128] *= 1e-3                                    # tiny scales (fp16 subnormal range) in group 0
     wq, s, z = oracle.quantize_weight_uint4(w, gs)
     cols = (torch.arange(M) * 37 + 5) % K                 # spread over every group and nibble position
     x = torch.zeros(M, K, dtype=xdt)
     x[torch.arange(M), cols] = 1
+    return x, wq, s, z, gs, cols
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K", [(2, 1024), (4, 7168), (4, 1024), (48, 1024), (160, 1024)])
+# decode: K-split (M <= 2, 1024 <= K <= 6144) and item-split (the rest); streaming; tiled
+def test_w4a16_dequantized_weights_exact(gpu, M, K, xdt):
+    """One-hot activation rows make every output one dequantized weight (the MFMA adds zeros to a
+    single product), so each kernel's uint4 dequantization -- the nibble as an fp16 subnormal into
+    v_fma_mix_f32 -- is checked bit for bit against round_16(fmaf(q, s, -z s))."""
+    from powershard_amd import ops
+    x, wq, s, z, gs, cols = _one_hot_case(M, K, xdt)
     y = ops.gemm_w4a16(x.to(gpu), wq.to(gpu), s.to(gpu), z.to(gpu), gs, None, out_dtype=torch.float32).cpu()
     want = _fma_form_weights(wq, s, z, gs, cols, xdt).T
     bad = (y != want).sum().item()
     assert bad == 0, f"{bad} of {y.numel()} dequantized weights differ"
+
+
+def test_w4a16_decode_inf_propagates(gpu):
+    """An infinite activation in a decode row (the K-split kernel: M = 2, K = 2048) gives what x @ W^T
+    gives with the 16-bit dequantized weights: +-inf where the weight at that k is nonzero (its sign
+    times the activation's), NaN where it is zero; the other row stays within the bar."""
+    from powershard_amd import ops
+    M, N, K, gs = 2, 640, 2048, 128
+    x = heavy_rows(M, K, seed=77, outlier_frac=0)
+    w = torch.randn(N, K, generator=seeded(78)) * 0.02
+    wq, s, z = oracle.quantize_weight_uint4(w, gs)
+    x[1, 700] = float("-inf")
+    y = ops.gemm_w4a16(x.to(gpu), wq.to(gpu), s.to(gpu), z.to(gpu), gs, None, out_dtype=torch.float32).cpu()
+    wd = oracle.dequant_uint4(wq, s, z, gs, out_dtype=torch.bfloat16).double()
+    col = wd[:, 700]
+    want = torch.where(col == 0, torch.tensor(float("nan"), dtype=torch.float64),
+                       torch.where(col > 0, torch.tensor(float("-inf"), dtype=torch.float64),
+                                   torch.tensor(float("inf"), dtype=torch.float64)))
+    got = y[1].double()
+    assert torch.equal(torch.isnan(got), torch.isnan(want)), "NaN pattern"
+    fin = ~torch.isnan(want)
+    assert torch.equal(got[fin], want[fin]), "infinities and their signs"
+    ref0 = oracle.gemm_wonly(x[:1], oracle.dequant_uint4(wq, s, z, gs, out_dtype=torch.bfloat16), None, None,
+                             out_dtype=torch.float32)
+    rms = ref0.pow(2).mean().sqrt().item()
+    assert (y[:1] - ref0).abs().max().item() <= 1e-2 * rms
 
 
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
