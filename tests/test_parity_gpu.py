@@ -315,6 +315,31 @@ def test_gemm_w4a16_split_k(gpu, M, N, K, xdt):
     assert_fp32_path(y32.cpu()[rows], yb.cpu()[rows], _wonly_rows(x, wd, b, rows), f"w4a16 split-K {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("kind,M,N,K", [("w4", 128, 25600, 5120), ("w4", 1024, 5120, 5120), ("w8", 1024, 5120, 5120),
+                                         ("w4", 1, 25600, 5120), ("w4", 5, 25600, 5120)])
+def test_gemm_wonly_repeat_bit_identical(gpu, kind, M, N, K):
+    """100 calls in a row give bit-identical fp32 outputs: the stream-K shapes of the tiled kernel
+    (whose partial tiles once came back stale now and then, 2-20 elements per 48-80 calls, until
+    the ordering of their stores and reads was fixed) and the decode kernels (K-split at M = 1,
+    item-split at M = 5), whose cross-wave sums are in a fixed order."""
+    from powershard_amd import ops
+    print(f"repeat {kind} {M}x{N}x{K}", flush=True)
+    x = heavy_rows(M, K, seed=98 + M, outlier_frac=0).to(gpu)
+    w = torch.randn(N, K, generator=seeded(99)) * 0.02
+    b = (torch.randn(N, generator=seeded(100)) * 0.01).to(torch.bfloat16).to(gpu)
+    if kind == "w4":
+        wq, s, z = oracle.quantize_weight_uint4(w, 128)
+        args = (x, wq.to(gpu), s.to(gpu), z.to(gpu), 128, b)
+        call = lambda: ops.gemm_w4a16(*args, out_dtype=torch.float32)
+    else:
+        q, s = oracle.quantize_weight_int8(w, False)
+        args = (x, q.to(gpu), s.to(gpu), b)
+        call = lambda: ops.gemm_w8a16(*args, out_dtype=torch.float32)
+    y0 = call()
+    diffs = [int((call().view(torch.int32) != y0.view(torch.int32)).sum()) for _ in range(100)]
+    assert sum(diffs) == 0, f"calls differing from the first: {[(i, d) for i, d in enumerate(diffs) if d][:5]}"
+
+
 @pytest.mark.parametrize("M,N,K", [(200, 1024, 2048), (1024, 5120, 5120), (100, 40960, 4096)])
 def test_gemm_w8a16_split_k(gpu, M, N, K):
     """K split across workgroups for the int8 weights: 128-row tiles in K parts (200 x 1024 x 2048)
